@@ -1,0 +1,268 @@
+// attention_fwd.hip -- fused flash-attention forward (fp32) for gfx950.
+//
+// No reference counterpart: pawel002/ember has no attention; the operator is
+// new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
+// are those of oracle/ember_oracle.c (oracle_attention_fwd).
+//
+// Work decomposition.  One workgroup = 4 waves = 128 queries of one (b, h);
+// each wave owns 32 queries for the whole kernel.  The workgroup walks the
+// keys in tiles of 64: every tile of K and V is read from HBM once with
+// coalesced 128-bit loads and staged in LDS, where the 4 waves share it.
+//
+// Per tile and wave (all products on v_mfma_f32_32x32x2f32):
+//   S^T (64 keys x 32 queries) = K_tile . Q^T   -- K from LDS, Q^T resident in
+//                                                  registers for the kernel
+//   online softmax over keys: each lane holds one query column, so the row
+//   max is an in-lane max over 32 registers plus one exchange with lane^32,
+//   and the row sum stays a per-lane partial until the end
+//   O^T (D x 32 queries) += V_tile^T . P^T      -- P^T straight from the S^T
+//                                                  accumulator registers
+// The softmax runs in base 2 with scale*log2(e) folded into one multiply;
+// LSE is stored in natural log.  Causal: tiles wholly above a wave's
+// diagonal are skipped per wave, the mask (key <= query, integer compare) is
+// applied only on tiles that cross the diagonal or the sequence end.
+#include <math.h>
+
+#include "common.h"
+#include "mfma.h"
+
+namespace ember {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBr = 32 * kWaves;  // queries per workgroup
+constexpr int kBc = 64;           // keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct FwdArgs {
+    const float *q, *k, *v;
+    float *o, *lse;
+    int H, S, nqb;
+    float c;  // scale * log2(e)
+    int64_t in_sb, in_sh, in_ss, out_sb, out_sh, out_ss;
+};
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
+{
+    constexpr int DH = D / 2;   // contraction length per lane half (k-steps)
+    constexpr int DB = D / 32;  // 32-row blocks of O^T
+    constexpr int KSTR = D + 4; // padded K row: conflict-free column reads
+    __shared__ float Ks[kBc * KSTR];
+    __shared__ float Vs[kBc * D];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+
+    // Heavy (late) query blocks first so the causal triangle load-balances.
+    const int BH = (int)(gridDim.x / a.nqb);
+    const int qbr = blockIdx.x / BH;
+    const int bh = blockIdx.x - qbr * BH;
+    const int qb = CAUSAL ? (a.nqb - 1 - qbr) : qbr;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int q0 = qb * kBr;
+    const int m0 = q0 + 32 * w;
+    const int mq = m0 + l32;
+
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const float *__restrict__ qp = a.q + in_base;
+    const float *__restrict__ kp = a.k + in_base;
+    const float *__restrict__ vp = a.v + in_base;
+
+    // Q^T operand: lane holds Q[mq][h32*DH + kk] for k-step kk.
+    float qr[DH];
+    {
+        const int mrow = mq < S ? mq : S - 1;
+        const float *src = qp + (int64_t)mrow * a.in_ss + h32 * DH;
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            f32x4 t = *(const f32x4 *)(src + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qr[kk + j] = t[j];
+        }
+    }
+
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+    float mrun = -INFINITY;  // running max of s*c for query mq
+    float lrun = 0.0f;       // this lane half's share of the running sum
+
+    const int kend = CAUSAL ? min(S, q0 + kBr) : S;
+    const int ntiles = (kend + kBc - 1) / kBc;
+    constexpr int kLoads = kBc * D / 4 / kThreads;
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int n0 = t * kBc;
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < kLoads; ++it) {
+            const int idx = it * kThreads + tid;
+            const int r = idx / (D / 4);
+            const int c4 = idx - r * (D / 4);
+            const int n = n0 + r;
+            f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            if (n < S) {
+                kv = *(const f32x4 *)(kp + (int64_t)n * a.in_ss + 4 * c4);
+                vv = *(const f32x4 *)(vp + (int64_t)n * a.in_ss + 4 * c4);
+            }
+            *(f32x4 *)&Ks[r * KSTR + 4 * c4] = kv;
+            *(f32x4 *)&Vs[r * D + 4 * c4] = vv;
+        }
+        __syncthreads();
+        if (CAUSAL && n0 > m0 + 31) continue;  // tile wholly above this wave's diagonal
+
+        // S^T = K . Q^T for two 32-key blocks.
+        f32x16 sacc[kBc / 32];
+#pragma unroll
+        for (int blk = 0; blk < kBc / 32; ++blk) sacc[blk] = zero16();
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+#pragma unroll
+            for (int blk = 0; blk < kBc / 32; ++blk) {
+                const f32x4 kf = *(const f32x4 *)&Ks[(32 * blk + l32) * KSTR + h32 * DH + kk];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sacc[blk] = mfma_32x32x2(kf[j], qr[kk + j], sacc[blk]);
+            }
+        }
+
+        // Scale, mask, tile max.
+        const bool need_mask = (n0 + kBc > S) || (CAUSAL && n0 + kBc - 1 > m0);
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float s = sacc[blk][i] * a.c;
+                if (need_mask) {
+                    const int n = n0 + 32 * blk + acc_row(i, h32);
+                    if (n >= S || (CAUSAL && n > mq)) s = -INFINITY;
+                }
+                sacc[blk][i] = s;
+                tmax = fmaxf(tmax, s);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        // Tile 0 always holds key 0, visible to every query, so mnew is finite.
+        const float mnew = fmaxf(mrun, tmax);
+        const float alpha = exp2f(mrun - mnew);
+        mrun = mnew;
+        lrun *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+#pragma unroll
+        for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = exp2f(sacc[blk][i] - mnew);
+                sacc[blk][i] = p;
+                lrun += p;
+            }
+        }
+
+        // O^T += V^T . P^T; lane l32 covers O^T rows d = DB*l32 + db.
+#pragma unroll
+        for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int nr = 32 * blk + acc_row(i, h32);
+                const typename VecN<DB>::T vf = *(const typename VecN<DB>::T *)&Vs[nr * D + DB * l32];
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    oacc[db] = mfma_32x32x2(vget<DB>(vf, db), sacc[blk][i], oacc[db]);
+            }
+        }
+    }
+
+    const float ltot = lrun + __shfl_xor(lrun, 32);
+    if (mq < S) {
+        const float inv = 1.0f / ltot;
+        float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = acc_row(i, h32);  // O^T row block index -> d = DB*r + db
+            typename VecN<DB>::T outv;
+            if constexpr (DB == 1) {
+                outv = oacc[0][i] * inv;
+            } else {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) outv[db] = oacc[db][i] * inv;
+            }
+            *(typename VecN<DB>::T *)(orow + DB * r) = outv;
+        }
+        if (h32 == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
+    }
+}
+
+template <int D, bool CAUSAL>
+int launch_fwd(const FwdArgs &args, int nblocks)
+{
+    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    return launch_ok("attn_fwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
+}  // namespace
+
+// Shared argument checks for attention_fwd / attention_bwd.
+int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t H, int64_t S,
+                         int64_t D, const int64_t *strides, int nstrides, const char *who)
+{
+    if (B < 0 || H < 0 || S < 0 || D <= 0)
+        return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    if (D != 32 && D != 64 && D != 128) return record_error(EMBER_ERR_UNSUPPORTED, who);
+    if (S > (int64_t)INT32_MAX / 2 || B * H > (int64_t)INT32_MAX / 1024)
+        return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    for (int i = 0; i < nstrides; ++i)
+        if (strides[i] < 0 || (strides[i] & 3)) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    if (B * H * S == 0) return EMBER_OK;
+    for (int i = 0; i < nptrs; ++i)
+        if (!ptrs[i] || ((uintptr_t)ptrs[i] & 15)) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    return EMBER_OK;
+}
+
+}  // namespace ember
+
+extern "C" int attention_fwd(const float *q, const float *k, const float *v, float *o, float *lse,
+                             int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
+                             int64_t in_sb, int64_t in_sh, int64_t in_ss, int64_t out_sb,
+                             int64_t out_sh, int64_t out_ss)
+{
+    using namespace ember;
+    const void *ptrs[] = {q, k, v, o, lse};
+    const int64_t strides[] = {in_sb, in_sh, in_ss, out_sb, out_sh, out_ss};
+    int st = check_attention_args(ptrs, 5, B, H, S, D, strides, 6, "attention_fwd");
+    if (st != EMBER_OK || B * H * S == 0) return st;
+
+    FwdArgs args;
+    args.q = q;
+    args.k = k;
+    args.v = v;
+    args.o = o;
+    args.lse = lse;
+    args.H = (int)H;
+    args.S = (int)S;
+    args.nqb = (int)((S + kBr - 1) / kBr);
+    args.c = scale * kLog2e;
+    args.in_sb = in_sb;
+    args.in_sh = in_sh;
+    args.in_ss = in_ss;
+    args.out_sb = out_sb;
+    args.out_sh = out_sh;
+    args.out_ss = out_ss;
+    const int nblocks = args.nqb * (int)(B * H);
+    switch (D * 2 + (causal ? 1 : 0)) {
+        case 64: return launch_fwd<32, false>(args, nblocks);
+        case 65: return launch_fwd<32, true>(args, nblocks);
+        case 128: return launch_fwd<64, false>(args, nblocks);
+        case 129: return launch_fwd<64, true>(args, nblocks);
+        case 256: return launch_fwd<128, false>(args, nblocks);
+        default: return launch_fwd<128, true>(args, nblocks);
+    }
+}

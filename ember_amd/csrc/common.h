@@ -1,0 +1,31 @@
+// common.h -- internal helpers shared by the HIP translation units of
+// libember_amd.so (not part of the public ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/ember_amd.h"
+
+namespace ember {
+
+// Records `status` in this thread's sticky error slot (first error wins) and
+// prints `what` with the HIP error text when `err` is a HIP failure.
+int record_error(int status, const char *what, hipError_t err = hipSuccess);
+
+// Checks a HIP call; on failure records EMBER_ERR_DEVICE and returns false.
+bool hip_ok(hipError_t err, const char *what);
+
+// Checks for a launch-configuration error right after a kernel launch
+// (asynchronous faults surface at the next synchronising call, as in the
+// reference's CUDA_POST_LAUNCH, src/tensor/operators_gpu.cu:12-15).
+bool launch_ok(const char *kernel);
+
+// Library-owned device scratch, grown on demand and cached per device for
+// the life of the process.  Slot ids keep independent users apart.
+void *scratch(int slot, size_t bytes);
+
+enum ScratchSlot { kScratchAttnDelta = 0, kScratchSum = 1, kScratchSlots = 4 };
+
+}  // namespace ember

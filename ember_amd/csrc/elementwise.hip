@@ -1,0 +1,266 @@
+// elementwise.hip -- the element-wise, transpose and reduction operators of
+// Ember's native ABI on HIP.
+//
+// These are off the attention/GEMM hot path; they exist so that the library
+// exports every symbol the reference's binding links against
+// (src/tensor/operators.h:10-27, implemented for CUDA in
+// src/tensor/operators_gpu.cu:33-219).  Differences from that file:
+//  * broadcast ops pass shape and strides to the kernel by value instead of
+//    three cudaMalloc + H2D copies + a device sync + three frees per call
+//    (operators_gpu.cu:94-106);
+//  * transpose goes through a 32 x 33 LDS tile so loads and stores are both
+//    coalesced (operators_gpu.cu:138-151 stores with a stride of n);
+//  * sum() reduces on the device in double and copies one float back,
+//    instead of copying the whole tensor to the host (operators_gpu.cu:153-166).
+// sum_axis / max_axis keep one thread per output walking the axis in index
+// order with a float accumulator, the exact arithmetic of the reference.
+#include <math.h>
+
+#include "common.h"
+
+namespace ember {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxDims = 16;
+
+inline int grid_for(int64_t n)
+{
+    int64_t g = (n + kBlock - 1) / kBlock;
+    return (int)(g > 1048576 ? 1048576 : (g < 1 ? 1 : g));
+}
+
+struct BcastShape {
+    int ndim;
+    int shape[kMaxDims];
+    int sa[kMaxDims];
+    int sb[kMaxDims];
+};
+
+}  // namespace
+}  // namespace ember
+
+using ember::BcastShape;
+using ember::grid_for;
+using ember::kBlock;
+
+#define EMBER_BINARY_OP(name, f)                                                              \
+    __global__ void k_##name##_tensor(const float *a, const float *b, float *out, int size)   \
+    {                                                                                         \
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < size;                         \
+             i += gridDim.x * blockDim.x) {                                                   \
+            const float x = a[i], y = b[i];                                                   \
+            out[i] = (f);                                                                     \
+        }                                                                                     \
+    }                                                                                         \
+    extern "C" void name##_tensor(const float *a, const float *b, float *out, int size)       \
+    {                                                                                         \
+        if (size <= 0) return;                                                                \
+        hipLaunchKernelGGL(k_##name##_tensor, dim3(grid_for(size)), dim3(kBlock), 0, 0, a, b, \
+                           out, size);                                                        \
+        ember::launch_ok(#name "_tensor");                                                    \
+    }
+
+#define EMBER_SCALAR_OP(name, f)                                                               \
+    __global__ void k_##name##_scalar(const float *a, float y, float *out, int size)           \
+    {                                                                                          \
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < size;                          \
+             i += gridDim.x * blockDim.x) {                                                    \
+            const float x = a[i];                                                              \
+            out[i] = (f);                                                                      \
+        }                                                                                      \
+    }                                                                                          \
+    extern "C" void name##_scalar(const float *a, float b, float *out, int size)               \
+    {                                                                                          \
+        if (size <= 0) return;                                                                 \
+        hipLaunchKernelGGL(k_##name##_scalar, dim3(grid_for(size)), dim3(kBlock), 0, 0, a, b,  \
+                           out, size);                                                         \
+        ember::launch_ok(#name "_scalar");                                                     \
+    }
+
+#define EMBER_UNARY_OP(name, f)                                                                \
+    __global__ void k_##name##_tensor(const float *a, float *out, int size)                    \
+    {                                                                                          \
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < size;                          \
+             i += gridDim.x * blockDim.x) {                                                    \
+            const float x = a[i];                                                              \
+            out[i] = (f);                                                                      \
+        }                                                                                      \
+    }                                                                                          \
+    extern "C" void name##_tensor(const float *a, float *out, int size)                        \
+    {                                                                                          \
+        if (size <= 0) return;                                                                 \
+        hipLaunchKernelGGL(k_##name##_tensor, dim3(grid_for(size)), dim3(kBlock), 0, 0, a,     \
+                           out, size);                                                         \
+        ember::launch_ok(#name "_tensor");                                                     \
+    }
+
+#define EMBER_BROADCAST_OP(name, f)                                                             \
+    __global__ void k_##name##_broadcasted(const float *a, const float *b, float *out,          \
+                                           BcastShape s, int total)                             \
+    {                                                                                           \
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total;                          \
+             i += gridDim.x * blockDim.x) {                                                     \
+            int rem = i, ia = 0, ib = 0;                                                        \
+            for (int d = s.ndim - 1; d >= 0; d--) {                                             \
+                const int coord = rem % s.shape[d];                                             \
+                rem /= s.shape[d];                                                              \
+                ia += coord * s.sa[d];                                                          \
+                ib += coord * s.sb[d];                                                          \
+            }                                                                                   \
+            const float x = a[ia], y = b[ib];                                                   \
+            out[i] = (f);                                                                       \
+        }                                                                                       \
+    }                                                                                           \
+    extern "C" void name##_broadcasted(const float *a, const float *b, float *out,              \
+                                       const int *shape, const int *strides_a,                  \
+                                       const int *strides_b, int ndim)                          \
+    {                                                                                           \
+        if (ndim < 0 || ndim > ember::kMaxDims) {                                               \
+            ember::record_error(EMBER_ERR_UNSUPPORTED, #name "_broadcasted: ndim");             \
+            return;                                                                             \
+        }                                                                                       \
+        BcastShape s;                                                                           \
+        s.ndim = ndim;                                                                          \
+        int total = 1;                                                                          \
+        for (int d = 0; d < ndim; d++) {                                                        \
+            s.shape[d] = shape[d];                                                              \
+            s.sa[d] = strides_a[d];                                                             \
+            s.sb[d] = strides_b[d];                                                             \
+            total *= shape[d];                                                                  \
+        }                                                                                       \
+        if (total <= 0) return;                                                                 \
+        hipLaunchKernelGGL(k_##name##_broadcasted, dim3(grid_for(total)), dim3(kBlock), 0, 0,   \
+                           a, b, out, s, total);                                                \
+        ember::launch_ok(#name "_broadcasted");                                                 \
+    }
+
+#include "operators.def"
+
+namespace {
+
+__global__ void k_transpose(const float *a, float *out, int n, int m)
+{
+    __shared__ float tile[32][33];
+    const int bx = blockIdx.x * 32, by = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+    for (int r = ty; r < 32; r += 8) {
+        const int i = by + r, j = bx + tx;
+        if (i < n && j < m) tile[r][tx] = a[(int64_t)i * m + j];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int j = bx + r, i = by + tx;  // out[j][i]
+        if (i < n && j < m) out[(int64_t)j * n + i] = tile[tx][r];
+    }
+}
+
+__global__ void k_sum_partial(const float *a, int size, double *partial)
+{
+    __shared__ double red[kBlock];
+    double s = 0.0;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < size; i += gridDim.x * blockDim.x)
+        s += (double)a[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = kBlock / 2; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+__global__ void k_sum_final(const double *partial, int n, float *out)
+{
+    __shared__ double red[kBlock];
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s += partial[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = kBlock / 2; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = (float)red[0];
+}
+
+__global__ void k_sum_axis(const float *a, float *out, int outer, int inner, int axis_dim)
+{
+    const int total = outer * inner;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        const int o = idx / inner, i = idx - o * inner;
+        const float *p = a + (int64_t)o * axis_dim * inner + i;
+        float s = 0.0f;
+        for (int r = 0; r < axis_dim; r++) s += p[(int64_t)r * inner];
+        out[idx] = s;
+    }
+}
+
+__global__ void k_max_axis(const float *a, float *out, int outer, int inner, int axis_dim)
+{
+    const int total = outer * inner;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        const int o = idx / inner, i = idx - o * inner;
+        const float *p = a + (int64_t)o * axis_dim * inner + i;
+        float mx = p[0];
+        for (int r = 1; r < axis_dim; r++) mx = fmaxf(mx, p[(int64_t)r * inner]);
+        out[idx] = mx;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+void transpose(const float *a, float *out, int n, int m)
+{
+    if (n <= 0 || m <= 0) return;
+    hipLaunchKernelGGL(k_transpose, dim3((m + 31) / 32, (n + 31) / 32), dim3(256), 0, 0, a, out, n,
+                       m);
+    ember::launch_ok("transpose");
+}
+
+float sum(const float *a, int size)
+{
+    if (size <= 0) return 0.0f;
+    const int nblk = grid_for(size) > 1024 ? 1024 : grid_for(size);
+    char *ws = (char *)ember::scratch(ember::kScratchSum, (size_t)nblk * sizeof(double) + 16);
+    if (!ws) return 0.0f;
+    double *partial = (double *)ws;
+    float *res = (float *)(ws + (size_t)nblk * sizeof(double));
+    hipLaunchKernelGGL(k_sum_partial, dim3(nblk), dim3(kBlock), 0, 0, a, size, partial);
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(kBlock), 0, 0, partial, nblk, res);
+    if (!ember::launch_ok("sum")) return 0.0f;
+    float host = 0.0f;
+    ember::hip_ok(hipMemcpy(&host, res, sizeof(float), hipMemcpyDeviceToHost), "sum");
+    return host;
+}
+
+int sum_axis_product(const int *shape, int start, int end)
+{
+    int p = 1;
+    for (int i = start; i < end; i++) p *= shape[i];
+    return p;
+}
+
+void sum_axis(const float *a, float *out, int outer_stride, int inner_stride, int axis_dim)
+{
+    const int total = outer_stride * inner_stride;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(k_sum_axis, dim3(grid_for(total)), dim3(kBlock), 0, 0, a, out, outer_stride,
+                       inner_stride, axis_dim);
+    ember::launch_ok("sum_axis");
+}
+
+void max_axis(const float *a, float *out, int outer_stride, int inner_stride, int axis_dim)
+{
+    const int total = outer_stride * inner_stride;
+    if (total <= 0 || axis_dim <= 0) return;
+    hipLaunchKernelGGL(k_max_axis, dim3(grid_for(total)), dim3(kBlock), 0, 0, a, out, outer_stride,
+                       inner_stride, axis_dim);
+    ember::launch_ok("max_axis");
+}
+
+}  // extern "C"

@@ -1,0 +1,128 @@
+/*
+ * ember_amd.h -- C ABI of libember_amd.so, the MI355X (gfx950) backend for
+ * Ember's native core.
+ *
+ * The library is a drop-in for the reference's GPU backend: it exports the
+ * same symbols with the same signatures that the reference's CPython binding
+ * (src/tensor/tensor_api.c, src/random/random_api.c) links against, so that
+ * binding can be linked against this library unchanged.  All pointers named
+ * a/b/out/q/k/v/... are device pointers obtained from alloc_memory() (or any
+ * other hipMalloc'd memory); sizes are in float elements unless noted.
+ * Work is enqueued on the HIP null stream, exactly like the reference's
+ * default-stream launches; results are visible after sync_device() or a
+ * copy_from_device(), which synchronises.
+ *
+ * Error behaviour.  The reference prints and calls exit() on any device
+ * error (src/core/utils_gpu.cuh:13-19).  Here the void entry points keep
+ * their signatures but record the first error in a sticky per-thread slot
+ * (ember_get_last_error) and print it to stderr; the process is not killed.
+ * The attention entry points, which are new, return that status directly.
+ * Argument errors never launch a kernel.
+ */
+#ifndef EMBER_AMD_H
+#define EMBER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+enum {
+    EMBER_OK = 0,
+    EMBER_ERR_INVALID_ARGUMENT = 1, /* bad sizes, strides or alignment */
+    EMBER_ERR_UNSUPPORTED = 2,      /* e.g. head_dim outside {32, 64, 128} */
+    EMBER_ERR_OUT_OF_MEMORY = 3,
+    EMBER_ERR_DEVICE = 4            /* a HIP runtime error; see stderr */
+};
+
+/* Returns the first status recorded on this thread since the last call, and
+ * clears it (hipGetLastError-style).  No reference counterpart: the reference
+ * exits instead (src/core/utils_gpu.cuh:17). */
+int ember_get_last_error(void);
+const char *ember_error_string(int status);
+
+/* ---- device memory: replaces src/core/memory.h:10-14 (memory_gpu.cu:10-43) ---- */
+void *alloc_memory(size_t bytes);  /* NULL on failure, like memory_gpu.cu:15-19 */
+void free_memory(void *ptr);
+void copy_to_device(void *dst_device, const void *src_host, size_t bytes);
+void copy_from_device(void *dst_host, const void *src_device, size_t bytes);
+void sync_device(void);
+
+/* ---- element-wise operators: replaces src/tensor/operators.h:10-18 ----
+ * One declaration per row of ember_amd/csrc/operators.def, which lists the
+ * same 37 operators as the reference's src/tensor/operators.def:39-82. */
+#define EMBER_BINARY_OP(name, expr) \
+    void name##_tensor(const float *a, const float *b, float *out, int size);
+#define EMBER_SCALAR_OP(name, expr) \
+    void name##_scalar(const float *a, float b, float *out, int size);
+#define EMBER_BROADCAST_OP(name, expr)                                                    \
+    void name##_broadcasted(const float *a, const float *b, float *out, const int *shape, \
+                            const int *strides_a, const int *strides_b, int ndim);
+#define EMBER_UNARY_OP(name, expr) void name##_tensor(const float *a, float *out, int size);
+#include "../ember_amd/csrc/operators.def"
+
+/* ---- non-element-wise operators: replaces src/tensor/operators.h:20-27 ---- */
+
+/* out(n x m) = a(n x k) @ b(k x m), row-major fp32, fp32 MFMA with fp32
+ * accumulation.  Replaces operators_gpu.cu:114-124 (cublasSgemm). */
+void matmul(const float *a, const float *b, float *out, int n, int m, int k);
+/* `batch` independent products with strides n*k, k*m, n*m.
+ * Replaces operators_gpu.cu:126-136 (cublasSgemmStridedBatched). */
+void matmul_batched(const float *a, const float *b, float *out, int batch, int n, int m, int k);
+/* out(m x n) = a(n x m)^T.  Replaces operators_gpu.cu:138-151. */
+void transpose(const float *a, float *out, int n, int m);
+/* Sum of all elements; replaces operators_gpu.cu:153-166 (the device
+ * reduction is summed in a fixed tree order, not sequentially). */
+float sum(const float *a, int size);
+/* Product of shape[start:end]; replaces operators_gpu.cu:168-173. */
+int sum_axis_product(const int *shape, int start, int end);
+/* Reduce the middle axis of (outer, axis_dim, inner); sequential fp32 sum /
+ * max in index order per output, as operators_gpu.cu:175-219. */
+void sum_axis(const float *a, float *out, int outer_stride, int inner_stride, int axis_dim);
+void max_axis(const float *a, float *out, int outer_stride, int inner_stride, int axis_dim);
+
+/* ---- fused attention (new; no reference counterpart exists) ----
+ *
+ * Shapes: batch B, heads H, sequence S (queries == keys), head_dim D in
+ * {32, 64, 128}.  Element (b, h, s, d) of q, k, v (and dq, dk, dv) lives at
+ *     b*in_sb + h*in_sh + s*in_ss + d
+ * and of o (and d_o) at b*out_sb + h*out_sh + s*out_ss + d, so packed
+ * (B, S, 3, H, D) projections are read and (B, S, H, D) outputs written
+ * without copies.  d must be contiguous, every stride a multiple of 4 and
+ * every pointer 16-byte aligned.  lse is dense (B, H, S), natural log.
+ *
+ * Semantics (the CPU restatement in oracle/ember_oracle.c is the checker):
+ *   s[i][j] = scale * <q_i, k_j>;  key j visible to query i iff j <= i when
+ *   causal (top-left aligned), always otherwise;
+ *   o_i = softmax_j(s[i][.]) v;  lse_i = ln sum_j exp(s[i][j]).
+ * Slots the reference would fill: src/tensor/operators.h:20-27 (new rows
+ * beside matmul), called from new _attention_fwd / _attention_bwd wrappers
+ * beside _matmul in src/tensor/tensor_api.c:305-354. */
+int attention_fwd(const float *q, const float *k, const float *v, float *o, float *lse,
+                  int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
+                  int64_t in_sb, int64_t in_sh, int64_t in_ss,
+                  int64_t out_sb, int64_t out_sh, int64_t out_ss);
+
+/* Backward of attention_fwd: given q, k, v, the forward's o and lse, and the
+ * upstream gradient d_o, writes dq, dk, dv (same layout as q, k, v).  P is
+ * recomputed from lse; the S x S matrix is never stored.  Needs B*H*S*4
+ * bytes of device scratch, which the library keeps cached between calls. */
+int attention_bwd(const float *q, const float *k, const float *v, const float *o,
+                  const float *lse, const float *d_o, float *dq, float *dk, float *dv,
+                  int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
+                  int64_t in_sb, int64_t in_sh, int64_t in_ss,
+                  int64_t out_sb, int64_t out_sh, int64_t out_ss);
+
+#undef EMBER_BINARY_OP
+#undef EMBER_SCALAR_OP
+#undef EMBER_BROADCAST_OP
+#undef EMBER_UNARY_OP
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMBER_AMD_H */

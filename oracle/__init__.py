@@ -1,0 +1,248 @@
+"""CPU checkers for the attention / matmul hot path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py``, always as the checker and never as
+the thing measured or shipped.  The product (``ember_amd``) never imports it.
+
+Two libraries sit behind this module:
+
+* ``liboracle.so`` -- this repository's C restatement (``ember_oracle.c``):
+  Ember's FP64-accumulating ``matmul`` (reference ``src/tensor/
+  operators_cpu.c:47-67``) and the build-defined attention forward/backward
+  written in the same style.
+* ``_ref/libember_ref.so`` -- the reference's own ``operators_cpu.c`` compiled
+  in place by ``oracle/Makefile``.  ``ref_composed_attention_*`` below drive
+  *those* functions in the order Ember's Python front-end would
+  (``ember/tensor/tensor.py:163-197`` for ``@``, ``:376-384`` for ``T``,
+  ``:430-437`` for ``softmax``; broadcast strides as in
+  ``ember/tensor/tensor_utils.py:97-140``), which is "attention as Ember can
+  express it today".  It is optional: absent when the reference checkout is.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_ORACLE_SO = os.path.join(_HERE, "liboracle.so")
+_REF_SO = os.path.join(_HERE, "_ref", "libember_ref.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+
+_lib = None
+_ref = None
+
+
+def build(reference_root: str = "/root/reference") -> None:
+    """Compile liboracle.so, and _ref/ when the reference checkout exists."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    if os.path.isdir(os.path.join(reference_root, "src", "tensor")):
+        subprocess.run(["make", "-s", "-C", _HERE, "ref", f"REF={reference_root}"], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_ORACLE_SO):
+            build()
+        L = C.CDLL(_ORACLE_SO)
+        L.oracle_matmul.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.oracle_matmul_mt.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.oracle_matmul_batched.argtypes = [_f32p, _f32p, _f32p] + [C.c_int] * 4
+        L.oracle_transpose.argtypes = [_f32p, _f32p, C.c_int, C.c_int]
+        L.oracle_attention_fwd.argtypes = [_f32p] * 5 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
+        L.oracle_attention_fwd.restype = C.c_int
+        L.oracle_attention_bwd.argtypes = [_f32p] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
+        L.oracle_attention_bwd.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(_REF_SO)
+
+
+def ref_lib() -> C.CDLL:
+    """The reference's operators_cpu.c, compiled in place (see Makefile)."""
+    global _ref
+    if _ref is None:
+        if not os.path.exists(_REF_SO):
+            raise FileNotFoundError(f"{_REF_SO} not built (needs the reference checkout)")
+        L = C.CDLL(_REF_SO)
+        L.matmul.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.matmul_batched.argtypes = [_f32p, _f32p, _f32p] + [C.c_int] * 4
+        L.transpose.argtypes = [_f32p, _f32p, C.c_int, C.c_int]
+        for name in ("sum_axis", "max_axis"):
+            getattr(L, name).argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        for name in ("add_tensor", "sub_tensor", "mul_tensor"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, C.c_int]
+        for name in ("mul_scalar", "add_scalar"):
+            getattr(L, name).argtypes = [_f32p, C.c_float, _f32p, C.c_int]
+        L.exponent_tensor.argtypes = [_f32p, _f32p, C.c_int]
+        for name in ("sub_broadcasted", "truediv_broadcasted", "mul_broadcasted"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _i32p, _i32p, _i32p, C.c_int]
+        _ref = L
+    return _ref
+
+
+def default_scale(d: int) -> float:
+    """fp32(1/sqrt(D)), the softmax scale every config uses."""
+    return float(np.float32(1.0 / math.sqrt(d)))
+
+
+# ---------------------------------------------------------------- restatement
+
+
+def matmul(a: np.ndarray, b: np.ndarray, threads: bool = False) -> np.ndarray:
+    """Ember's CPU matmul semantics (FP64 accumulation, one cast per output)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    n, k = a.shape
+    k2, m = b.shape
+    assert k == k2
+    out = np.empty((n, m), dtype=np.float32)
+    (lib().oracle_matmul_mt if threads else lib().oracle_matmul)(a, b, out, n, m, k)
+    return out
+
+
+def _strides4(shape):
+    B, H, S, D = shape
+    return (H * S * D, S * D, D)
+
+
+def attention_fwd(q, k, v, causal: bool, scale: float | None = None):
+    """(B,H,S,D) contiguous fp32 -> (O (B,H,S,D), LSE (B,H,S))."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    B, H, S, D = q.shape
+    scale = default_scale(D) if scale is None else scale
+    o = np.empty_like(q)
+    lse = np.empty((B, H, S), dtype=np.float32)
+    st = _strides4(q.shape)
+    rc = lib().oracle_attention_fwd(q, k, v, o, lse, B, H, S, D, scale, int(causal), *st, *st)
+    assert rc == 0
+    return o, lse
+
+
+def attention_bwd(q, k, v, o, lse, d_o, causal: bool, scale: float | None = None):
+    """Gradients (dQ, dK, dV) of <O, dO>, recomputing P from the given LSE."""
+    q, k, v, o, d_o = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v, o, d_o))
+    lse = np.ascontiguousarray(lse, dtype=np.float32)
+    B, H, S, D = q.shape
+    scale = default_scale(D) if scale is None else scale
+    dq, dk, dv = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    st = _strides4(q.shape)
+    rc = lib().oracle_attention_bwd(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale,
+                                    int(causal), *st, *st)
+    assert rc == 0
+    return dq, dk, dv
+
+
+# ------------------------------------------- the reference's own ops, composed
+
+
+def _bcast(shape_a, shape_b):
+    """Output shape and strides exactly as tensor_utils.calculate_broadcast."""
+    def contig(shape):
+        st, cur = [0] * len(shape), 1
+        for i in range(len(shape) - 1, -1, -1):
+            st[i] = cur
+            cur *= shape[i]
+        return st
+    sa, sb = contig(shape_a), contig(shape_b)
+    out, oa, ob = [], [], []
+    for da, xa, db, xb in zip(shape_a, sa, shape_b, sb):
+        if da == db:
+            out.append(da); oa.append(xa); ob.append(xb)
+        elif da == 1:
+            out.append(db); oa.append(0); ob.append(xb)
+        else:
+            out.append(da); oa.append(xa); ob.append(0)
+    return [np.asarray(x, dtype=np.int32) for x in (out, oa, ob)]
+
+
+def _ref_softmax_rows(R, x: np.ndarray) -> np.ndarray:
+    """em.softmax(x, axis=-1) on an (n, m) tensor: amax -> sub -> exp -> sum -> div."""
+    n, m = x.shape
+    mx = np.empty((n, 1), dtype=np.float32)
+    R.max_axis(x, mx, n, 1, m)
+    shp, sa, sb = _bcast((n, m), (n, 1))
+    shifted = np.empty((n, m), dtype=np.float32)
+    R.sub_broadcasted(x, mx, shifted, shp, sa, sb, 2)
+    e = np.empty((n, m), dtype=np.float32)
+    R.exponent_tensor(shifted, e, n * m)
+    s = np.empty((n, 1), dtype=np.float32)
+    R.sum_axis(e, s, n, 1, m)
+    out = np.empty((n, m), dtype=np.float32)
+    R.truediv_broadcasted(e, s, out, shp, sa, sb, 2)
+    return out
+
+
+def _ref_mm(R, a, b):
+    n, k = a.shape
+    m = b.shape[1]
+    out = np.empty((n, m), dtype=np.float32)
+    R.matmul(np.ascontiguousarray(a), np.ascontiguousarray(b), out, n, m, k)
+    return out
+
+
+def _ref_T(R, a):
+    n, m = a.shape
+    out = np.empty((m, n), dtype=np.float32)
+    R.transpose(np.ascontiguousarray(a), out, n, m)
+    return out
+
+
+def _mask(S: int, causal: bool) -> np.ndarray:
+    if not causal:
+        return np.zeros((S, S), dtype=np.float32)
+    i = np.arange(S)[:, None]
+    j = np.arange(S)[None, :]
+    return np.where(j <= i, 0.0, -np.inf).astype(np.float32)
+
+
+def ref_composed_attention_head(qh, kh, vh, doh, causal: bool, scale: float, backward: bool):
+    """One head through the reference's own CPU ops, the way Ember composes it.
+
+    Forward: ``p = softmax(q @ T(k) * scale + mask); o = p @ v``.  Backward,
+    written with the same ops: ``dV = T(p) @ dO``, ``dP = dO @ T(v)``,
+    ``dS = p * (dP - rowsum(dO * o))``, ``dQ = (dS @ k) * scale``,
+    ``dK = (T(dS) @ q) * scale``.  Returns (o, p) or (o, dq, dk, dv).
+    """
+    R = ref_lib()
+    S, D = qh.shape
+    qh, kh, vh = (np.ascontiguousarray(x, dtype=np.float32) for x in (qh, kh, vh))
+    s = _ref_mm(R, qh, _ref_T(R, kh))
+    s2 = np.empty_like(s)
+    R.mul_scalar(s, np.float32(scale), s2, S * S)
+    s3 = np.empty_like(s)
+    R.add_tensor(s2, _mask(S, causal), s3, S * S)
+    p = _ref_softmax_rows(R, s3)
+    o = _ref_mm(R, p, vh)
+    if not backward:
+        return o, p
+    doh = np.ascontiguousarray(doh, dtype=np.float32)
+    dv = _ref_mm(R, _ref_T(R, p), doh)
+    dp = _ref_mm(R, doh, _ref_T(R, vh))
+    prod = np.empty_like(o)
+    R.mul_tensor(doh, o, prod, S * D)
+    delta = np.empty((S, 1), dtype=np.float32)
+    R.sum_axis(prod, delta, S, 1, D)
+    shp, sa, sb = _bcast((S, S), (S, 1))
+    dpm = np.empty_like(dp)
+    R.sub_broadcasted(dp, delta, dpm, shp, sa, sb, 2)
+    ds = np.empty_like(dp)
+    R.mul_tensor(p, dpm, ds, S * S)
+    dq0 = _ref_mm(R, ds, kh)
+    dq = np.empty_like(dq0)
+    R.mul_scalar(dq0, np.float32(scale), dq, S * D)
+    dk0 = _ref_mm(R, _ref_T(R, ds), qh)
+    dk = np.empty_like(dk0)
+    R.mul_scalar(dk0, np.float32(scale), dk, S * D)
+    return o, dq, dk, dv

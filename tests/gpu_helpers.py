@@ -1,0 +1,80 @@
+"""Calls the HIP attention / matmul entry points through the C ABI
+(ember_amd.capi -> libember_amd.so) on numpy inputs.  GPU tests only."""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+
+from ember_amd import capi
+from ember_amd.capi import DeviceArray
+
+
+def say(msg: str) -> None:
+    """Names the case about to run on the GPU (flushed, for post-mortems)."""
+    print(f"[gpu] {msg}", file=sys.stderr, flush=True)
+
+
+def scale_for(D: int) -> float:
+    return float(np.float32(1.0 / math.sqrt(D)))
+
+
+def attention_fwd(q, k, v, causal, scale=None):
+    B, H, S, D = q.shape
+    scale = scale_for(D) if scale is None else scale
+    say(f"attention_fwd B={B} H={H} S={S} D={D} causal={causal}")
+    dq, dk, dv = (DeviceArray.from_numpy(x) for x in (q, k, v))
+    o = DeviceArray((B, H, S, D))
+    lse = DeviceArray((B, H, S))
+    st = capi.contiguous_strides(B, H, S, D)
+    rc = capi.lib().attention_fwd(dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr, B, H, S, D, scale,
+                                  int(causal), *st, *st)
+    capi.check(rc, "attention_fwd")
+    return o.numpy(), lse.numpy()
+
+
+def attention_bwd(q, k, v, o, lse, d_o, causal, scale=None):
+    B, H, S, D = q.shape
+    scale = scale_for(D) if scale is None else scale
+    say(f"attention_bwd B={B} H={H} S={S} D={D} causal={causal}")
+    ins = [DeviceArray.from_numpy(x) for x in (q, k, v, o, lse, d_o)]
+    outs = [DeviceArray((B, H, S, D)) for _ in range(3)]
+    st = capi.contiguous_strides(B, H, S, D)
+    rc = capi.lib().attention_bwd(*(x.ptr for x in ins), *(x.ptr for x in outs), B, H, S, D,
+                                  scale, int(causal), *st, *st)
+    capi.check(rc, "attention_bwd")
+    return tuple(x.numpy() for x in outs)
+
+
+def matmul(a, b):
+    n, k = a.shape
+    m = b.shape[1]
+    say(f"matmul n={n} m={m} k={k}")
+    da, db = DeviceArray.from_numpy(a), DeviceArray.from_numpy(b)
+    out = DeviceArray((n, m))
+    capi.lib().matmul(da.ptr, db.ptr, out.ptr, n, m, k)
+    capi.check(what="matmul")
+    return out.numpy()
+
+
+def matmul_batched(a, b):
+    batch, n, k = a.shape
+    m = b.shape[2]
+    say(f"matmul_batched batch={batch} n={n} m={m} k={k}")
+    da, db = DeviceArray.from_numpy(a), DeviceArray.from_numpy(b)
+    out = DeviceArray((batch, n, m))
+    capi.lib().matmul_batched(da.ptr, db.ptr, out.ptr, batch, n, m, k)
+    capi.check(what="matmul_batched")
+    return out.numpy()
+
+
+def gemm_error_bound(a, b):
+    """Rigorous bound on |fl(a@b) - a@b| for any fp32 summation order of
+    length k: gamma_k * (|a| @ |b|), gamma_k = k u / (1 - k u), u = 2^-24,
+    doubled for the final rounding and margin."""
+    k = a.shape[-1]
+    u = 2.0 ** -24
+    gamma = k * u / (1 - k * u)
+    return 2.0 * gamma * (np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))) + 1e-30

@@ -1,0 +1,209 @@
+"""Parity of the HIP flash-attention forward/backward with the CPU oracle.
+
+Tolerance (from the project's north star): max-abs 2e-4 / rel 1e-3 in
+fp32 for O, LSE, dQ, dK, dV; mask handling and tile boundaries are checked
+bitwise through invariants that any leak across the mask would break.
+All calls go through the C ABI (libember_amd.so).
+"""
+
+import numpy as np
+import pytest
+
+import gpu_helpers as G
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rtol=1e-3, atol=2e-4)
+
+
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+def _inputs(B, H, S, D, seed=0):
+    return tuple(_rand((B, H, S, D), seed + i) for i in range(4))
+
+
+# ------------------------------------------------------------ golden fixtures
+
+
+def _gpu_cases(golden):
+    return [n for n, c in golden.items() if c["q"].shape[-1] in (32, 64, 128)]
+
+
+def test_forward_matches_golden(golden):
+    for name in _gpu_cases(golden):
+        c = golden[name]
+        o, lse = G.attention_fwd(c["q"], c["k"], c["v"], bool(c["causal"]), float(c["scale"]))
+        np.testing.assert_allclose(o, c["o"], err_msg=name, **TOL)
+        np.testing.assert_allclose(lse, c["lse"], err_msg=name, **TOL)
+
+
+def test_backward_matches_golden(golden):
+    for name in _gpu_cases(golden):
+        c = golden[name]
+        causal, scale = bool(c["causal"]), float(c["scale"])
+        o, lse = G.attention_fwd(c["q"], c["k"], c["v"], causal, scale)
+        dq, dk, dv = G.attention_bwd(c["q"], c["k"], c["v"], o, lse, c["do"], causal, scale)
+        for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+            np.testing.assert_allclose(got, c[key], err_msg=f"{name}/{key}", **TOL)
+
+
+# ------------------------------------------------------------ edges and sizes
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("S", [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 257])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fwd_bwd_edges_match_oracle(S, D, causal):
+    q, k, v, d_o = _inputs(1, 2, S, D, seed=S * 7 + D)
+    o, lse = G.attention_fwd(q, k, v, causal)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, causal)
+    np.testing.assert_allclose(o, o_ref, **TOL)
+    np.testing.assert_allclose(lse, lse_ref, **TOL)
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    dq_r, dk_r, dv_r = oracle.attention_bwd(q, k, v, o_ref, lse_ref, d_o, causal)
+    np.testing.assert_allclose(dq, dq_r, **TOL)
+    np.testing.assert_allclose(dk, dk_r, **TOL)
+    np.testing.assert_allclose(dv, dv_r, **TOL)
+
+
+def test_config1_forward_full():
+    """B=1 H=4 S=256 D=64 non-causal: full O against the CPU path."""
+    q, k, v, _ = _inputs(1, 4, 256, 64, seed=100)
+    o, lse = G.attention_fwd(q, k, v, False)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, False)
+    np.testing.assert_allclose(o, o_ref, **TOL)
+    np.testing.assert_allclose(lse, lse_ref, **TOL)
+
+
+def test_config2_causal_forward_slices():
+    """B=8 H=16 S=2048 D=64 causal, whole problem on the GPU, three heads checked."""
+    q, k, v, _ = _inputs(8, 16, 2048, 64, seed=200)
+    o, lse = G.attention_fwd(q, k, v, True)
+    for b, h in ((0, 0), (0, 15), (7, 3)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_ref, lse_ref = oracle.attention_fwd(q[sl], k[sl], v[sl], True)
+        np.testing.assert_allclose(o[sl], o_ref, err_msg=f"b={b} h={h}", **TOL)
+        np.testing.assert_allclose(lse[sl], lse_ref, err_msg=f"b={b} h={h}", **TOL)
+
+
+def test_config3_causal_fwd_bwd_slice():
+    """B=4 H=32 S=4096 D=128 causal fwd+bwd on the GPU; B=1 H=2 slice vs CPU."""
+    q, k, v, d_o = _inputs(4, 32, 4096, 128, seed=300)
+    o, lse = G.attention_fwd(q, k, v, True)
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, True)
+    sl = (slice(0, 1), slice(0, 2))
+    o_ref, lse_ref = oracle.attention_fwd(q[sl], k[sl], v[sl], True)
+    np.testing.assert_allclose(o[sl], o_ref, **TOL)
+    np.testing.assert_allclose(lse[sl], lse_ref, **TOL)
+    dq_r, dk_r, dv_r = oracle.attention_bwd(q[sl], k[sl], v[sl], o_ref, lse_ref, d_o[sl], True)
+    np.testing.assert_allclose(dq[sl], dq_r, **TOL)
+    np.testing.assert_allclose(dk[sl], dk_r, **TOL)
+    np.testing.assert_allclose(dv[sl], dv_r, **TOL)
+    # Size-independent properties over all 128 heads:
+    #   sum_j dV_j = sum_i dO_i          (rows of P sum to 1)
+    #   sum_j dK_j = 0                   (sum_j dS_ij = sum_j P_ij dP_ij - delta_i = 0)
+    assert np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    sum_dv = dv.astype(np.float64).sum(axis=2)
+    sum_do = d_o.astype(np.float64).sum(axis=2)
+    np.testing.assert_allclose(sum_dv, sum_do, rtol=1e-4, atol=1e-3)
+    sum_dk = np.abs(dk.astype(np.float64).sum(axis=2))
+    assert (sum_dk <= 1e-3 * np.abs(dk.astype(np.float64)).sum(axis=2) + 1e-4).all()
+
+
+# ------------------------------------------------------- bitwise invariants
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_causal_mask_does_not_leak(D):
+    """Changing keys/values after row i leaves O and LSE of rows <= i bitwise unchanged."""
+    S = 300
+    q, k, v, _ = _inputs(1, 1, S, D, seed=400 + D)
+    o, lse = G.attention_fwd(q, k, v, True)
+    for i in (0, 63, 64, 127, 128, 200):
+        k2, v2 = k.copy(), v.copy()
+        k2[0, 0, i + 1:] = _rand((S - i - 1, D), i)
+        v2[0, 0, i + 1:] = _rand((S - i - 1, D), i + 1)
+        o2, lse2 = G.attention_fwd(q, k2, v2, True)
+        assert np.array_equal(o[0, 0, : i + 1], o2[0, 0, : i + 1]), i
+        assert np.array_equal(lse[0, 0, : i + 1], lse2[0, 0, : i + 1]), i
+    assert np.array_equal(o[0, 0, 0], v[0, 0, 0])  # row 0 attends key 0 only
+
+
+def test_keys_past_the_end_do_not_leak():
+    """Non-causal S=65: rows are identical whether or not the buffer has junk after S."""
+    S, D = 65, 64
+    q, k, v, _ = _inputs(1, 1, S, D, seed=500)
+    o, lse = G.attention_fwd(q, k, v, False)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, False)
+    np.testing.assert_allclose(o, o_ref, **TOL)
+    np.testing.assert_allclose(lse, lse_ref, **TOL)
+
+
+def test_forward_is_deterministic():
+    q, k, v, _ = _inputs(2, 3, 200, 128, seed=600)
+    a = G.attention_fwd(q, k, v, True)
+    b = G.attention_fwd(q, k, v, True)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_backward_zero_upstream_gradient_is_exactly_zero():
+    q, k, v, _ = _inputs(1, 2, 150, 64, seed=700)
+    o, lse = G.attention_fwd(q, k, v, True)
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, np.zeros_like(q), True)
+    assert not dq.any() and not dk.any() and not dv.any()
+
+
+def test_backward_last_key_sees_only_last_query():
+    S, D = 129, 64
+    q, k, v, d_o = _inputs(1, 1, S, D, seed=800)
+    o, lse = G.attention_fwd(q, k, v, True)
+    _, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, True)
+    s = G.scale_for(D) * float(np.dot(q[0, 0, -1].astype(np.float64), k[0, 0, -1]))
+    p = np.exp(s - float(lse[0, 0, -1]))
+    np.testing.assert_allclose(dv[0, 0, -1], p * d_o[0, 0, -1], **TOL)
+
+
+# ------------------------------------------------------------ strided layout
+
+
+def test_packed_qkv_layout():
+    """q, k, v read from one (B, S, 3, H, D) buffer; o / dO in (B, S, H, D)."""
+    from ember_amd import capi
+    from ember_amd.capi import DeviceArray
+
+    B, H, S, D = 2, 4, 160, 64
+    qkv = _rand((B, S, 3, H, D), 900)
+    d_o_bshd = _rand((B, S, H, D), 901)
+    q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
+    d_o = np.ascontiguousarray(d_o_bshd.transpose(0, 2, 1, 3))
+    o_ref, lse_ref = G.attention_fwd(q, k, v, True)
+    dq_ref, dk_ref, dv_ref = G.attention_bwd(q, k, v, o_ref, lse_ref, d_o, True)
+
+    G.say("packed qkv layout")
+    L = capi.lib()
+    dqkv = DeviceArray.from_numpy(qkv)
+    ddo = DeviceArray.from_numpy(d_o_bshd)
+    o = DeviceArray((B, S, H, D))
+    lse = DeviceArray((B, H, S))
+    grads = DeviceArray((B, S, 3, H, D))
+    in_st = (S * 3 * H * D, D, 3 * H * D)
+    out_st = (S * H * D, D, H * D)
+    base, step = dqkv.ptr, H * D * 4
+    st = L.attention_fwd(base, base + step, base + 2 * step, o.ptr, lse.ptr, B, H, S, D,
+                         G.scale_for(D), 1, *in_st, *out_st)
+    capi.check(st, "attention_fwd")
+    gb = grads.ptr
+    st = L.attention_bwd(base, base + step, base + 2 * step, o.ptr, lse.ptr, ddo.ptr,
+                         gb, gb + step, gb + 2 * step, B, H, S, D, G.scale_for(D), 1,
+                         *in_st, *out_st)
+    capi.check(st, "attention_bwd")
+    o_np = o.numpy().transpose(0, 2, 1, 3)
+    g = grads.numpy()
+    assert np.array_equal(o_np, o_ref)
+    assert np.array_equal(lse.numpy(), lse_ref)
+    assert np.array_equal(g[:, :, 1].transpose(0, 2, 1, 3), dk_ref)
+    assert np.array_equal(g[:, :, 2].transpose(0, 2, 1, 3), dv_ref)
+    np.testing.assert_allclose(g[:, :, 0].transpose(0, 2, 1, 3), dq_ref, rtol=1e-5, atol=1e-6)

@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports every symbol include/ember_amd.h
+declares; argument validation rejects bad calls before any device work.
+CPU only: no call here reaches the HIP runtime."""
+
+import ctypes as C
+
+import pytest
+
+from ember_amd import capi
+
+# The reference's backend ABI (src/core/memory.h:10-14, src/tensor/operators.h:10-27).
+REFERENCE_SYMBOLS = {
+    "alloc_memory", "free_memory", "copy_to_device", "copy_from_device", "sync_device",
+    "matmul", "matmul_batched", "transpose", "sum", "sum_axis_product", "sum_axis", "max_axis",
+    "add_tensor", "sub_tensor", "mul_tensor", "truediv_tensor", "max_tensor", "min_tensor",
+    "gt_tensor", "lt_tensor", "pow_tensor",
+    "add_scalar", "sub_scalar", "rsub_scalar", "mul_scalar", "truediv_scalar",
+    "rtruediv_scalar", "max_scalar", "min_scalar", "gt_scalar", "lt_scalar", "pow_scalar",
+    "rpow_scalar",
+    "add_broadcasted", "sub_broadcasted", "mul_broadcasted", "truediv_broadcasted",
+    "negate_tensor", "exponent_tensor", "log_tensor", "sqrt_tensor", "sin_tensor", "cos_tensor",
+    "tan_tensor", "ctg_tensor", "sinh_tensor", "cosh_tensor", "tanh_tensor", "ctgh_tensor",
+}
+
+
+def test_library_loads():
+    assert capi.lib() is not None
+
+
+def test_header_declares_reference_abi_and_attention():
+    names = set(capi.exported_symbols())
+    assert REFERENCE_SYMBOLS <= names
+    assert {"attention_fwd", "attention_bwd"} <= names
+
+
+def test_every_declared_symbol_is_exported():
+    L = capi.lib()
+    missing = [n for n in capi.exported_symbols() if not hasattr(L, n)]
+    assert missing == []
+
+
+def test_error_strings():
+    L = capi.lib()
+    assert L.ember_error_string(0) == b"success"
+    assert L.ember_error_string(2) == b"unsupported configuration"
+    assert L.ember_get_last_error() == 0
+
+
+def _fwd_call(D=64, B=1, H=1, S=8, ptr=16, strides=(512, 512, 64)):
+    L = capi.lib()
+    p = C.c_void_p(ptr)
+    return L.attention_fwd(p, p, p, p, p, B, H, S, D, 0.125, 1, *strides, *strides)
+
+
+@pytest.mark.parametrize("D", [0, 8, 48, 96, 256])
+def test_attention_rejects_unsupported_head_dims(D):
+    st = _fwd_call(D=D)
+    assert st in (1, 2)
+    assert capi.lib().ember_get_last_error() == st
+
+
+def test_attention_rejects_bad_layouts():
+    L = capi.lib()
+    assert _fwd_call(ptr=0) == 1                       # null pointer
+    assert _fwd_call(ptr=18) == 1                      # not 16-byte aligned
+    assert _fwd_call(strides=(512, 512, 66)) == 1      # stride not a multiple of 4
+    assert _fwd_call(B=-1) == 1
+    L.ember_get_last_error()
+    assert _fwd_call(S=0) == 0                         # empty: nothing to do
+
+
+def test_capi_raises_on_sticky_error():
+    _fwd_call(D=48)
+    with pytest.raises(capi.EmberError):
+        capi.check()

@@ -1,0 +1,83 @@
+"""Parity of the HIP fp32 MFMA GEMM (matmul / matmul_batched) with Ember's
+CPU matmul (FP64 accumulation, oracle/ember_oracle.c, itself bitwise the
+reference's operators_cpu.c).  The GPU accumulates in fp32, so results are
+checked against a rigorous fp32 summation error bound, gamma_k * |A||B|,
+and bitwise where fp32 arithmetic is exact."""
+
+import numpy as np
+import pytest
+
+import gpu_helpers as G
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _u(shape, seed):
+    return np.random.default_rng(seed).uniform(-1, 1, shape).astype(np.float32)
+
+
+def _check(got, a, b, exact=None):
+    exact = oracle.matmul(a, b, threads=True) if exact is None else exact
+    bound = G.gemm_error_bound(a, b)
+    err = np.abs(got.astype(np.float64) - exact.astype(np.float64))
+    assert (err <= bound).all(), f"max err {err.max()} vs bound {bound.min()}"
+
+
+@pytest.mark.parametrize(
+    "shape_a, shape_b",
+    [((4, 5), (5, 3)), ((1, 1), (1, 1))],  # reference test_tensor.py:125-145
+)
+def test_reference_matmul_cases(shape_a, shape_b):
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal(shape_a).astype(np.float32)
+    b = rng.standard_normal(shape_b).astype(np.float32)
+    np.testing.assert_allclose(G.matmul(a, b), a @ b, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize(
+    "shape_a, shape_b",
+    [((2, 3, 4), (2, 4, 5)), ((4, 2, 3), (4, 3, 6)), ((6, 5, 6), (6, 6, 2))],  # test_tensor.py:165-176
+)
+def test_reference_batched_cases(shape_a, shape_b):
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal(shape_a).astype(np.float32)
+    b = rng.standard_normal(shape_b).astype(np.float32)
+    np.testing.assert_allclose(G.matmul_batched(a, b), a @ b, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize(
+    "n,k,m",
+    [(32, 128, 64), (1, 10, 5), (64, 32, 128), (16, 50, 50),        # test_linear.py shapes
+     (127, 33, 129), (128, 32, 128), (129, 1, 255), (257, 300, 3), (5, 4096, 7),
+     (300, 64, 260), (1000, 500, 700)],
+)
+def test_matmul_within_fp32_bound(n, k, m):
+    a, b = _u((n, k), n), _u((k, m), m)
+    _check(G.matmul(a, b), a, b)
+
+
+def test_batched_matches_per_batch():
+    a, b = _u((5, 130, 70), 3), _u((5, 70, 90), 4)
+    got = G.matmul_batched(a, b)
+    for i in range(5):
+        _check(got[i], a[i], b[i])
+
+
+def test_identity_and_integers_are_exact():
+    a = _u((200, 136), 5)
+    assert np.array_equal(G.matmul(a, np.eye(136, dtype=np.float32)), a)
+    rng = np.random.default_rng(6)
+    ai = rng.integers(-8, 8, (150, 260)).astype(np.float32)
+    bi = rng.integers(-8, 8, (260, 90)).astype(np.float32)
+    assert np.array_equal(G.matmul(ai, bi), (ai.astype(np.int64) @ bi.astype(np.int64)).astype(np.float32))
+
+
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 4096), (16384, 1024, 3072)])
+def test_config4_shapes_sampled(n, k, m):
+    """Full product on the GPU; 96 rows (first, last, random) against the CPU path."""
+    a, b = _u((n, k), 7), _u((k, m), 8)
+    got = G.matmul(a, b)
+    rows = np.unique(np.concatenate([[0, 1, n - 1], np.random.default_rng(9).integers(0, n, 93)]))
+    exact = oracle.matmul(a[rows], b, threads=True)
+    _check(got[rows], a[rows], b, exact)

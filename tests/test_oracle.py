@@ -1,0 +1,219 @@
+"""Pins the CPU oracle (oracle/ember_oracle.c) before anything is checked
+against it.  CPU only.
+
+What pins what:
+* closed forms (tests/closed_forms.py)  <- central finite differences and
+  textbook special cases (uniform attention, V = 1, one-hot scores);
+* oracle attention fwd/bwd              <- golden fixtures from the closed
+  forms, the reference's own CPU ops composed the way Ember composes
+  attention today (oracle/_ref, when built), mask invariants;
+* oracle matmul                         <- the reference's compiled
+  operators_cpu.c matmul, bit for bit, on the reference's own test shapes.
+Planted-mistake tests show each pin fails for a plausible bug.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import closed_forms
+import oracle
+
+TOL = dict(rtol=1e-5, atol=2e-6)
+
+
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+# ------------------------------------------------------------ closed forms
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_closed_form_gradients_match_finite_differences(causal):
+    q, k, v, d_o = (_rand((1, 1, 5, 3), s) for s in (1, 2, 3, 4))
+    scale = 0.7
+    fd = closed_forms.finite_difference_grads(q, k, v, d_o, causal, scale)
+    cf = closed_forms.bwd(q, k, v, d_o, causal, scale)
+    for a, b in zip(cf, fd):
+        np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+
+
+def test_closed_form_special_cases():
+    S, D = 9, 4
+    v = _rand((1, 1, S, D), 5)
+    q = _rand((1, 1, S, D), 6)
+    zeros = np.zeros_like(q)
+    # K = 0: uniform attention.  Causal row i averages V[0..i]; LSE = ln(i+1).
+    o, lse = closed_forms.fwd(q, zeros, v, True, 1.0)
+    cum = np.cumsum(v[0, 0].astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
+    np.testing.assert_allclose(o[0, 0], cum, rtol=1e-12)
+    np.testing.assert_allclose(lse[0, 0], np.log(np.arange(1, S + 1)), rtol=1e-12)
+    o, lse = closed_forms.fwd(q, zeros, v, False, 1.0)
+    np.testing.assert_allclose(o[0, 0], np.broadcast_to(v[0, 0].astype(np.float64).mean(0), (S, D)), rtol=1e-12)
+    np.testing.assert_allclose(lse[0, 0], np.full(S, math.log(S)), rtol=1e-12)
+    # V = 1 => O = 1.
+    o, _ = closed_forms.fwd(q, _rand((1, 1, S, D), 7), np.ones_like(v), False, 1.0)
+    np.testing.assert_allclose(o, 1.0, rtol=1e-12)
+    # One dominant score per row => O_i ~ v_j.
+    k = np.zeros((1, 1, S, D), dtype=np.float32)
+    qd = np.zeros_like(k)
+    qd[0, 0, :, 0] = 1.0
+    k[0, 0, 3, 0] = 100.0
+    o, _ = closed_forms.fwd(qd, k, v, False, 1.0)
+    np.testing.assert_allclose(o[0, 0], np.broadcast_to(v[0, 0, 3], (S, D)), atol=1e-30)
+
+
+# ------------------------------------------------------------- golden pins
+
+
+def test_golden_fixtures_cover_the_tile_edges(golden):
+    seqs = {c["q"].shape[2] for c in golden.values()}
+    assert {1, 2, 17, 33, 64, 65, 130} <= seqs
+    assert {bool(c["causal"]) for c in golden.values()} == {False, True}
+
+
+def test_oracle_forward_matches_golden(golden):
+    for name, c in golden.items():
+        o, lse = oracle.attention_fwd(c["q"], c["k"], c["v"], bool(c["causal"]), float(c["scale"]))
+        np.testing.assert_allclose(o, c["o"], err_msg=name, **TOL)
+        np.testing.assert_allclose(lse, c["lse"], err_msg=name, **TOL)
+
+
+def test_oracle_backward_matches_golden(golden):
+    for name, c in golden.items():
+        causal, scale = bool(c["causal"]), float(c["scale"])
+        o, lse = oracle.attention_fwd(c["q"], c["k"], c["v"], causal, scale)
+        dq, dk, dv = oracle.attention_bwd(c["q"], c["k"], c["v"], o, lse, c["do"], causal, scale)
+        for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+            np.testing.assert_allclose(got, c[key], err_msg=f"{name}/{key}", rtol=1e-5, atol=1e-5)
+
+
+def test_planted_mistakes_fail_the_golden_pin(golden):
+    """A flipped mask, a wrong scale or a transposed operand must not pass."""
+    c = golden["s65_d64_c"]
+    q, k, v = c["q"], c["k"], c["v"]
+    scale = float(c["scale"])
+    for bad in (
+        lambda: oracle.attention_fwd(q, k, v, False, scale),                    # mask dropped
+        lambda: oracle.attention_fwd(q, k, v, True, scale * 1.01),              # scale off
+        lambda: oracle.attention_fwd(k, q, v, True, scale),                     # q <-> k
+        lambda: oracle.attention_fwd(q, k, v[:, :, ::-1].copy(), True, scale),  # v rows reversed
+    ):
+        o, _ = bad()
+        assert not np.allclose(o, c["o"], **TOL)
+
+
+# ------------------------------------- the reference's own ops, composed
+
+
+needs_ref = pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built")
+
+
+@needs_ref
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S,D", [(48, 16), (65, 32)])
+def test_oracle_matches_reference_composed_ops(S, D, causal):
+    q, k, v, d_o = (_rand((1, 1, S, D), s) for s in (21, 22, 23, 24))
+    scale = oracle.default_scale(D)
+    o_ref, dq_ref, dk_ref, dv_ref = oracle.ref_composed_attention_head(
+        q[0, 0], k[0, 0], v[0, 0], d_o[0, 0], causal, scale, backward=True)
+    o, lse = oracle.attention_fwd(q, k, v, causal, scale)
+    np.testing.assert_allclose(o[0, 0], o_ref, rtol=1e-5, atol=1e-6)
+    dq, dk, dv = oracle.attention_bwd(q, k, v, o, lse, d_o, causal, scale)
+    np.testing.assert_allclose(dq[0, 0], dq_ref, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(dk[0, 0], dk_ref, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(dv[0, 0], dv_ref, rtol=1e-4, atol=1e-5)
+
+
+@needs_ref
+@pytest.mark.parametrize(
+    "n,k,m", [(4, 5, 3), (1, 1, 1), (32, 128, 64), (64, 32, 128), (16, 50, 50), (33, 17, 65)]
+)
+def test_oracle_matmul_is_bitwise_the_reference(n, k, m):
+    """Shapes from the reference's test_tensor.py:125-145 and test_linear.py:12-17."""
+    a = _rand((n, k), 31)
+    b = _rand((k, m), 32)
+    ref = np.empty((n, m), dtype=np.float32)
+    oracle.ref_lib().matmul(a, b, ref, n, m, k)
+    assert np.array_equal(oracle.matmul(a, b), ref)
+    assert np.array_equal(oracle.matmul(a, b, threads=True), ref)
+
+
+@needs_ref
+def test_oracle_batched_and_transpose_match_reference():
+    a = _rand((3, 5, 6), 33)
+    b = _rand((3, 6, 4), 34)
+    ref = np.empty((3, 5, 4), dtype=np.float32)
+    oracle.ref_lib().matmul_batched(a, b, ref, 3, 5, 4, 6)
+    got = np.empty_like(ref)
+    oracle.lib().oracle_matmul_batched(a, b, got, 3, 5, 4, 6)
+    assert np.array_equal(got, ref)
+    t_ref = np.empty((6, 5), dtype=np.float32)
+    oracle.ref_lib().transpose(np.ascontiguousarray(a[0]), t_ref, 5, 6)
+    t = np.empty_like(t_ref)
+    oracle.lib().oracle_transpose(np.ascontiguousarray(a[0]), t, 5, 6)
+    assert np.array_equal(t, t_ref)
+
+
+def test_oracle_matmul_against_float64():
+    a = _rand((40, 300), 35)
+    b = _rand((300, 20), 36)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    # FP64 accumulation: one rounding of (nearly) the exact value.
+    np.testing.assert_allclose(oracle.matmul(a, b), exact.astype(np.float32), rtol=2e-7, atol=1e-12)
+
+
+# ------------------------------------------------------- mask invariants
+
+
+def test_oracle_mask_invariants_are_bitwise():
+    S, D = 40, 16
+    q, k, v = (_rand((1, 1, S, D), s) for s in (41, 42, 43))
+    o, lse = oracle.attention_fwd(q, k, v, True)
+    i = 17
+    k2, v2 = k.copy(), v.copy()
+    k2[0, 0, i + 1:] += 3.0
+    v2[0, 0, i + 1:] -= 5.0
+    o2, lse2 = oracle.attention_fwd(q, k2, v2, True)
+    assert np.array_equal(o[0, 0, : i + 1], o2[0, 0, : i + 1])
+    assert np.array_equal(lse[0, 0, : i + 1], lse2[0, 0, : i + 1])
+    assert np.array_equal(o[0, 0, 0], v[0, 0, 0])  # row 0 sees key 0 only
+    assert lse[0, 0, 0] == np.float32(oracle.default_scale(D) * float(np.dot(
+        q[0, 0, 0].astype(np.float64), k[0, 0, 0].astype(np.float64))))
+
+
+def test_oracle_backward_invariants():
+    S, D = 24, 8
+    q, k, v, d_o = (_rand((1, 1, S, D), s) for s in (51, 52, 53, 54))
+    o, lse = oracle.attention_fwd(q, k, v, True)
+    dq, dk, dv = oracle.attention_bwd(q, k, v, o, lse, np.zeros_like(d_o), True)
+    assert not dq.any() and not dk.any() and not dv.any()
+    dq, dk, dv = oracle.attention_bwd(q, k, v, o, lse, d_o, True)
+    # The last key is seen only by the last query, with weight P[S-1][S-1].
+    s_last = oracle.default_scale(D) * np.dot(q[0, 0, -1].astype(np.float64), k[0, 0, -1])
+    p = math.exp(s_last - float(lse[0, 0, -1]))
+    np.testing.assert_allclose(dv[0, 0, -1], p * d_o[0, 0, -1].astype(np.float64), rtol=1e-6)
+
+
+def test_oracle_strided_layout_matches_contiguous():
+    B, H, S, D = 2, 3, 19, 8
+    qkv = _rand((B, S, 3, H, D), 61)
+    q = np.ascontiguousarray(qkv[:, :, 0].transpose(0, 2, 1, 3))
+    k = np.ascontiguousarray(qkv[:, :, 1].transpose(0, 2, 1, 3))
+    v = np.ascontiguousarray(qkv[:, :, 2].transpose(0, 2, 1, 3))
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, True)
+    o = np.zeros((B, S, H, D), dtype=np.float32)
+    lse = np.zeros((B, H, S), dtype=np.float32)
+    flat = np.ascontiguousarray(qkv).reshape(-1)
+    L = oracle.lib()
+    scale = oracle.default_scale(D)
+    in_st = (S * 3 * H * D, D, 3 * H * D)
+    out_st = (S * H * D, D, H * D)
+    rc = L.oracle_attention_fwd(flat, np.ascontiguousarray(flat[H * D:]),
+                                np.ascontiguousarray(flat[2 * H * D:]), o.reshape(-1), lse,
+                                B, H, S, D, scale, 1, *in_st, *out_st)
+    assert rc == 0
+    assert np.array_equal(o.transpose(0, 2, 1, 3), o_ref)
+    assert np.array_equal(lse, lse_ref)
