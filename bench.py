@@ -1,0 +1,262 @@
+"""Benchmark: fused causal attention forward+backward, fp32, on one MI355X.
+
+Workload (the config the metric is quoted on):
+B=4, H=32, S=4096, D=128, causal, Q/K/V/dO ~ N(0,1) seeded, scale 1/sqrt(D).
+One step = attention_fwd + attention_bwd through the C ABI of
+libember_amd.so on inputs already resident in HBM.
+
+Throughput uses the FlashAttention-2 flop convention: fwd 4*B*H*S^2*D,
+bwd 2.5x fwd, both halved for causal -> 7*B*H*S^2*D per step (1.924e12).
+Timing: W warm-up steps, then K steps between two device synchronisations;
+per-entry-point durations come from HIP events recorded on the null stream,
+which is the stream every kernel of the library is launched on.
+
+The CPU baseline runs Ember's own CPU operators (the reference's
+operators_cpu.c, compiled in place under oracle/_ref) composed the way Ember
+expresses attention today, on a bounded sample: one full-size head
+(S=4096, D=128) per host thread, fwd+bwd.  It falls back to this
+repository's C restatement (oracle/ember_oracle.c) when _ref is absent.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import threading
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from ember_amd import capi  # noqa: E402
+from ember_amd.capi import DeviceArray  # noqa: E402
+
+PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (AMD spec)
+PEAK_HBM_GBS = 8000.0
+METRIC = "attention fwd+bwd TFLOP/s at S=4096 D=128 fp32, % of MFMA fp32 peak, 1 GPU"
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "attn_bwd_c3_traffic.json")
+
+
+class HipEvents:
+    """hipEvent timing on the null stream via libamdhip64 (plumbing only)."""
+
+    def __init__(self):
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        self.hip = C.CDLL(os.path.join(rocm, "lib", "libamdhip64.so"))
+        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def create(self, n):
+        evs = []
+        for _ in range(n):
+            e = C.c_void_p()
+            assert self.hip.hipEventCreate(C.byref(e)) == 0
+            evs.append(e)
+        return evs
+
+    def record(self, e):
+        assert self.hip.hipEventRecord(e, None) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.hip.hipEventSynchronize(b) == 0
+        t = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(t), a, b) == 0
+        return float(t.value)
+
+
+def attention_flops(B, H, S, D, causal=True):
+    fwd = 4.0 * B * H * S * S * D * (0.5 if causal else 1.0)
+    return fwd, 2.5 * fwd
+
+
+def cpu_baseline(S, D, threads):
+    """Times Ember's CPU path on `threads` heads (one per thread), fwd+bwd."""
+    import oracle
+
+    rng = np.random.default_rng(1234)
+    heads = [tuple(rng.standard_normal((S, D)).astype(np.float32) for _ in range(4))
+             for _ in range(threads)]
+    scale = oracle.default_scale(D)
+    kind = "reference" if oracle.ref_available() else "port"
+
+    def run(h):
+        q, k, v, d_o = h
+        if kind == "reference":
+            oracle.ref_composed_attention_head(q, k, v, d_o, True, scale, backward=True)
+        else:
+            o, lse = oracle.attention_fwd(q[None, None], k[None, None], v[None, None], True, scale)
+            oracle.attention_bwd(q[None, None], k[None, None], v[None, None], o, lse,
+                                 d_o[None, None], True, scale)
+
+    ts = [threading.Thread(target=run, args=(h,)) for h in heads]
+    t0 = time.perf_counter()
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    wall = time.perf_counter() - t0
+    fwd, bwd = attention_flops(1, threads, S, D)
+    what = ("the reference's operators_cpu.c ops composed as Ember would (matmul, transpose, "
+            "mul_scalar, add_tensor mask, softmax via max_axis/sub/exp/sum_axis/div; "
+            "backward with the same ops)") if kind == "reference" else \
+        "oracle/ember_oracle.c FP64 restatement"
+    return {
+        "value": (fwd + bwd) / wall / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": f"{threads} head(s) of S={S} D={D} causal fwd+bwd, one per thread, "
+                  f"{wall:.1f} s wall; {what}; flops counted as on the GPU (causal half)",
+        "wall_s": wall,
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=4)
+    ap.add_argument("--heads", type=int, default=32)
+    ap.add_argument("--seq", type=int, default=4096)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--non-causal", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="host threads (= heads) for the CPU baseline; 0 skips it")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="after the timed steps, run one plain copy-like kernel "
+                         "(negate_tensor: reads and writes N MiB) so rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE can be scaled against known bytes")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on exactly one GPU (no multi-GPU path); "
+              "use --gpus 1", file=sys.stderr)
+        return 2
+
+    B, H, S, D = args.batch, args.heads, args.seq, args.head_dim
+    causal = not args.non_causal
+    scale = float(np.float32(1.0 / math.sqrt(D)))
+    L = capi.lib()
+
+    rng = np.random.default_rng(0)
+    host = [rng.standard_normal((B, H, S, D), dtype=np.float32) for _ in range(4)]
+    q, k, v, d_o = (DeviceArray.from_numpy(x) for x in host)
+    del host
+    o = DeviceArray((B, H, S, D))
+    lse = DeviceArray((B, H, S))
+    dq, dk, dv = (DeviceArray((B, H, S, D)) for _ in range(3))
+    st = capi.contiguous_strides(B, H, S, D)
+
+    def fwd():
+        return L.attention_fwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, B, H, S, D, scale,
+                               int(causal), *st, *st)
+
+    def bwd():
+        return L.attention_bwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, d_o.ptr, dq.ptr, dk.ptr,
+                               dv.ptr, B, H, S, D, scale, int(causal), *st, *st)
+
+    ev = HipEvents()
+    for _ in range(args.warmup):
+        capi.check(fwd(), "attention_fwd")
+        capi.check(bwd(), "attention_bwd")
+    L.sync_device()
+    capi.check(what="warmup")
+
+    K = args.steps
+    marks = ev.create(2 * K + 1)
+    L.sync_device()
+    t0 = time.perf_counter()
+    ev.record(marks[0])
+    for i in range(K):
+        fwd()
+        ev.record(marks[2 * i + 1])
+        bwd()
+        ev.record(marks[2 * i + 2])
+    L.sync_device()
+    wall = time.perf_counter() - t0
+    capi.check(what="timed steps")
+
+    fwd_ms = [ev.elapsed_ms(marks[2 * i], marks[2 * i + 1]) for i in range(K)]
+    bwd_ms = [ev.elapsed_ms(marks[2 * i + 1], marks[2 * i + 2]) for i in range(K)]
+    total_ms = ev.elapsed_ms(marks[0], marks[2 * K])
+    ms_per_step = total_ms / K
+
+    out_ok = all(np.isfinite(x.numpy()).all() for x in (o, dq))
+    fwd_fl, bwd_fl = attention_flops(B, H, S, D, causal)
+    value = (fwd_fl + bwd_fl) / (ms_per_step * 1e-3) / 1e12
+    bwd_avg = sum(bwd_ms) / K
+    fwd_avg = sum(fwd_ms) / K
+    achieved = bwd_fl / (bwd_avg * 1e-3) / 1e12
+
+    traffic = None
+    if os.path.exists(PROFILE_TRAFFIC):
+        with open(PROFILE_TRAFFIC) as f:
+            prof = json.load(f)
+        if prof.get("workload") == f"B{B} H{H} S{S} D{D} causal={causal}":
+            traffic = prof.get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"causal attention fwd+bwd B={B} H={H} S={S} D={D} fp32"
+            if causal else f"attention fwd+bwd B={B} H={H} S={S} D={D} fp32",
+            "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": causal,
+            "flops_per_step": fwd_fl + bwd_fl,
+        },
+        "frac_of_fp32_mfma_peak": round(value / PEAK_FP32_MFMA_TFLOPS, 4),
+        "fwd_ms": round(fwd_avg, 4),
+        "bwd_ms": round(bwd_avg, 4),
+        "fwd_tflops": round(fwd_fl / (fwd_avg * 1e-3) / 1e12, 3),
+        "wall_s_timed": round(wall, 4),
+        "outputs_finite": bool(out_ok),
+        "roofline": {
+            "kernel": "attention_bwd (attn_bwd_pre + attn_bwd_kernel)",
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": traffic,
+        },
+    }
+    if args.copy_probe_mb > 0:
+        n = args.copy_probe_mb * (1 << 20) // 4
+        src, dst = DeviceArray((n,)), DeviceArray((n,))
+        L.negate_tensor.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        L.negate_tensor(src.ptr, dst.ptr, n)
+        L.sync_device()
+        capi.check(what="copy probe")
+        result["copy_probe_bytes"] = {"read": 4 * n, "write": 4 * n}
+
+    threads = args.cpu_threads
+    if threads is None:
+        threads = min(16, os.cpu_count() or 1)
+    if threads > 0:
+        result["cpu_baseline"] = cpu_baseline(S, D, threads)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

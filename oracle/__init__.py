@@ -42,9 +42,9 @@ _ref = None
 
 def build(reference_root: str = "/root/reference") -> None:
     """Compile liboracle.so, and _ref/ when the reference checkout exists."""
-    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle.so"], check=True)
     if os.path.isdir(os.path.join(reference_root, "src", "tensor")):
-        subprocess.run(["make", "-s", "-C", _HERE, "ref", f"REF={reference_root}"], check=True)
+        subprocess.run(["make", "-s", "-B", "-C", _HERE, "ref", f"REF={reference_root}"], check=True)
 
 
 def lib() -> C.CDLL:
