@@ -221,6 +221,9 @@ int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t 
         return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     for (int i = 0; i < nstrides; ++i)
         if (strides[i] < 0 || (strides[i] & 3)) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    // Row strides (the third of each triple) index rows with 32-bit offsets.
+    if (strides[2] >= (int64_t(1) << 24) || strides[5] >= (int64_t(1) << 24))
+        return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     if (B * H * S == 0) return EMBER_OK;
     for (int i = 0; i < nptrs; ++i)
         if (!ptrs[i] || ((uintptr_t)ptrs[i] & 15)) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
