@@ -27,12 +27,16 @@ LIB = os.path.join(PKG, "libember_amd.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
+# (source, extra hipcc flags).  -amdgpu-mfma-vgpr-form=1 keeps MFMA
+# accumulators in VGPRs; attention_bwd.hip explains which instantiations use
+# which form and why.
 HIP_SOURCES = [
-    "runtime.hip",
-    "elementwise.hip",
-    "gemm.hip",
-    "attention_fwd.hip",
-    "attention_bwd.hip",
+    ("runtime.hip", []),
+    ("elementwise.hip", []),
+    ("gemm.hip", []),
+    ("attention_fwd.hip", []),
+    ("attention_bwd.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]),
+    ("attention_bwd_c128.hip", []),
 ]
 
 HIP_FLAGS = [
@@ -66,18 +70,18 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(out + "\n")
 
 
-def _compile_hip(src: str, extra: list[str]) -> str:
+def _compile_hip(src: str, flags: list[str], extra: list[str]) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    _run([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
+    _run([HIPCC, *HIP_FLAGS, *flags, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 
 def build_library(extra_flags: list[str] | None = None) -> str:
     os.makedirs(BUILD, exist_ok=True)
     extra = list(extra_flags or [])
-    sources = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    sources = [(s, f) for s, f in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(lambda s: _compile_hip(s, extra), sources))
+        objs = list(ex.map(lambda sf: _compile_hip(sf[0], sf[1], extra), sources))
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)

@@ -1,0 +1,457 @@
+// attention_bwd_kernels.h -- kernels of the fused attention backward,
+// included by attention_bwd.hip and attention_bwd_c128.hip.
+//
+// No reference counterpart (pawel002/ember has no attention); semantics are
+// those of oracle/ember_oracle.c (oracle_attention_bwd): P is recomputed from
+// the forward's LSE, never stored.
+//
+// Two launches on the null stream:
+//  1. attn_bwd_pre (HBM-bound, one pass over O and dO): per query row
+//     lse2 = lse * log2(e) and delta = <dO, O> into a row-statistics scratch
+//     whose rows are padded per (b, h) to a multiple of 32 (padding rows get
+//     lse2 = +inf, delta = 0, so every P they enter is exactly 0); and
+//     dQ := 0 (dQ is accumulated with atomics).
+//  2. attn_bwd_kernel, K/V-stationary: one workgroup = 4 waves = 128 keys of
+//     one (b, h).  Each wave keeps K and V of its 32 keys resident in
+//     registers as MFMA B operands and accumulates dK, dV for them in
+//     registers.  The workgroup walks query blocks of 32 (causal: only the
+//     blocks at or below its keys) with Q, dO and the block's lse2 / delta
+//     staged in LDS:
+//        S  = Q K^T, dP = dO V^T           (C[m][n], keys on lanes)
+//        P  = exp2(S*c - lse2[m]), dS = P * (dP - delta[m])
+//        dV += P^T dO,  dK += dS^T Q       (P / dS registers are the A
+//                                           operands directly)
+//     dS of all 4 waves goes through LDS so that dQ(32 x D) = dS . K over the
+//     workgroup's 128 keys is one more MFMA product per wave, added to the
+//     global dQ with hardware fp32 atomics (dq must be device memory).
+//
+// Pipelining and instruction economy.  The next query block's Q, dO, lse2
+// and delta are copied HBM -> LDS directly (gfx950 global_load_lds_dwordx4,
+// no registers) into the second of two buffers while the current block is
+// multiplied.  All LDS tiles use padded rows (Q/dO: D+4 floats, dS: 128+4;
+// K: rows of D with the second half of the keys shifted by 32 floats) rather
+// than XOR swizzles, chosen so that every LDS access in the loop is a per-lane
+// base register plus a compile-time offset: the loop then spends its VALU
+// issue slots on the softmax and not on address arithmetic.  Blocks that
+// cross the causal diagonal or the last key hold the mask; all others run a
+// mask-free path.
+#pragma once
+
+#include <math.h>
+
+#include "common.h"
+#include "mfma.h"
+
+namespace ember {
+
+int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t H, int64_t S,
+                         int64_t D, const int64_t *strides, int nstrides, const char *who);
+
+struct BwdArgs {
+    const float *q, *k, *v, *o, *lse, *dout;
+    float *dq, *dk, *dv;
+    float *lse2, *delta;  // row statistics, (B*H, S_pad) each
+    int H, S, S_pad, nkb;
+    float c;      // scale * log2(e)
+    float scale;
+    int64_t in_sb, in_sh, in_ss, out_sb, out_sh, out_ss;
+};
+
+// attention_bwd_c128.hip: the causal D = 128 launch (a translation unit of
+// its own, see the file comment).
+int launch_bwd_causal_d128(const BwdArgs &args, int64_t rows_pad, int nblocks);
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBkw = 32;            // keys per wave
+constexpr int kBk = kBkw * kWaves;  // keys per workgroup
+constexpr int kBq = 32;             // queries per step
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Row statistics and dQ := 0.  D/4 threads per (padded) row.
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_pre(BwdArgs a, int64_t rows_pad)
+{
+    constexpr int TPR = D / 4;
+    constexpr int RPB = 256 / TPR;
+    const int sub = threadIdx.x % TPR;
+    const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
+    if (row >= rows_pad) return;  // whole TPR-lane groups retire together
+    const int64_t bh = row / a.S_pad;
+    const int m = (int)(row - bh * a.S_pad);
+    if (m >= a.S) {
+        if (sub == 0) {
+            a.lse2[row] = INFINITY;
+            a.delta[row] = 0.0f;
+        }
+        return;
+    }
+    const int b = (int)(bh / a.H);
+    const int hh = (int)(bh - (int64_t)b * a.H);
+    const int64_t ooff = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)m * a.out_ss + 4 * sub;
+    const f32x4 ov = *(const f32x4 *)(a.o + ooff);
+    const f32x4 gv = *(const f32x4 *)(a.dout + ooff);
+    float s = ov[0] * gv[0] + ov[1] * gv[1] + ov[2] * gv[2] + ov[3] * gv[3];
+#pragma unroll
+    for (int off = TPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (sub == 0) {
+        a.delta[row] = s;
+        a.lse2[row] = a.lse[bh * a.S + m] * kLog2e;
+    }
+    const int64_t qoff = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub;
+    *(f32x4 *)(a.dq + qoff) = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's data
+// lands at lds + 16*l bytes (gfx950 global_load_lds_dwordx4; lds must be
+// wave-uniform).
+__device__ __forceinline__ void dma16(const float *src, float *lds)
+{
+    typedef __attribute__((address_space(1))) void gvoid;
+    typedef __attribute__((address_space(3))) void lvoid;
+    __builtin_amdgcn_global_load_lds((gvoid *)src, (lvoid *)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): every vector-memory operation this wave issued,
+// including LDS-bound copies, has completed.
+__device__ __forceinline__ void wait_vmem()
+{
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+template <int D>
+struct BwdLayout {
+    static constexpr int DB = D / 32;
+    static constexpr int QSTR = D + 4;                // padded Q / dO row
+    static constexpr int QROWCH = QSTR / 4;           // 16-byte chunks per padded row
+    static constexpr int QCHUNKS = kBq * QROWCH;      // chunks per Q / dO tile
+    static constexpr int QDMA = (QCHUNKS + 63) / 64;  // 1 KiB copies per tile
+    static constexpr int QBUF = QDMA * 256;           // floats reserved per tile
+    static constexpr int SLOTS = (QDMA + kWaves - 1) / kWaves;  // copies per wave
+    static constexpr int SSTR = kBk + 4;              // padded dS row
+    static constexpr int NSPLIT = 4 / DB;             // waves sharing a 32-wide d block of dQ
+    static constexpr int NK = kBk / NSPLIT;           // keys each wave contracts for dQ
+    static constexpr int NKH = NK / 2;                // ... per lane half
+    // K row n at n*D + (n / NKH)*32: the two lane halves of the dQ product
+    // read rows NKH apart, which the shift puts 32 banks apart.
+    static constexpr int KALL = kBk * D + (kBk / NKH) * 32;
+};
+
+constexpr int kMaxSlots = 5;  // BwdLayout<128>::SLOTS
+
+// Loop-invariant state of one workgroup.
+struct BwdBlock {
+    const float *qp, *gp;      // q, dO at (b, h)
+    const float *l2p, *dlp;    // lse2, delta at (b, h)
+    float *dqp;                // dq at (b, h)
+    int S, nq, n0w, w;
+    int in_ss, out_ss;
+    // Per copy slot s (copy t = w + 4s of a tile): this lane's chunk as a
+    // source offset within the block for q and dO (-1: padding or slack,
+    // never read) and its row.
+    int qoff[kMaxSlots], goff[kMaxSlots], row[kMaxSlots];
+    bool key_tail;
+};
+
+// Copies query block m0's Q and dO tiles (padded rows) and its lse2 / delta
+// into one set of buffers.  Copy t of a tile fills chunks 64t .. 64t+63; a
+// padding or slack chunk reads row m0's first chunk (valid memory, never
+// used).  Rows past the end re-read row S-1; their lse2 is +inf, so they
+// contribute exactly 0.
+template <int D>
+__device__ __forceinline__ void bwd_fetch(const BwdBlock &k, int m0, float *__restrict__ qn,
+                                          float *__restrict__ gn, float *__restrict__ stn)
+{
+    typedef BwdLayout<D> L;
+    const float *qb = k.qp + (int64_t)m0 * k.in_ss;
+    const float *gb = k.gp + (int64_t)m0 * k.out_ss;
+    const int rmax = k.S - 1 - m0;  // rows beyond it are clamped to it
+#pragma unroll
+    for (int s = 0; s < L::SLOTS; ++s) {
+        const int t = k.w + kWaves * s;
+        if (t < L::QDMA) {
+            const int cl = k.row[s] > rmax ? rmax - k.row[s] : 0;
+            // Unsigned (non-negative) offsets from a wave-uniform base let the
+            // copy use scalar-base + 32-bit vector-offset addressing.
+            const unsigned qo = k.qoff[s] < 0 ? 0u : (unsigned)(k.qoff[s] + cl * k.in_ss);
+            const unsigned go = k.goff[s] < 0 ? 0u : (unsigned)(k.goff[s] + cl * k.out_ss);
+            dma16(qb + qo, qn + 256 * t);
+            dma16(gb + go, gn + 256 * t);
+        }
+    }
+    if (k.w == 0) {
+        const int lane = threadIdx.x & 63;
+        if (lane < 16) dma16(lane < 8 ? k.l2p + m0 + 4 * lane : k.dlp + m0 + 4 * (lane - 8), stn);
+    }
+}
+
+// One query block: phase 1 on (qs, gs, st), barrier, dS to LDS, barrier,
+// phase 2 (dQ); meanwhile the next block is copied into (qn, gn, stn).  The
+// buffers are distinct __restrict__ pointers so that the compiler can tell
+// the LDS-bound copies from the reads of the current buffers and does not
+// wait for them before every LDS read.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, int qb,
+                                         const float *__restrict__ qs,
+                                         const float *__restrict__ gs,
+                                         const float *__restrict__ st, float *__restrict__ ds,
+                                         float *__restrict__ qn, float *__restrict__ gn,
+                                         float *__restrict__ stn,
+                                         const float *__restrict__ kall, const float *kr,
+                                         const float *vr, f32x16 *dvacc, f32x16 *dkacc)
+{
+    typedef BwdLayout<D> L;
+    constexpr int DH = D / 2;
+    constexpr int DB = L::DB;
+    const int lane = threadIdx.x & 63;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    const int w = k.w;
+    const int m0 = qb * kBq;
+    const int S = k.S;
+
+    if (qb + 1 < k.nq) bwd_fetch<D>(k, m0 + kBq, qn, gn, stn);
+
+    // ---- phase 1: S, dP, P, dS; dV += P^T dO, dK += dS^T Q ----
+    f32x16 pacc;
+    const bool active = !CAUSAL || k.n0w <= m0 + kBq - 1;
+    if (active) {
+        f32x16 sacc = zero16();
+        pacc = zero16();
+        const int abase = l32 * L::QSTR + h32 * DH;
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            const f32x4 qf = *(const f32x4 *)&qs[abase + kk];
+            const f32x4 gf = *(const f32x4 *)&gs[abase + kk];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sacc = mfma_32x32x2(qf[j], kr[kk + j], sacc);
+                pacc = mfma_32x32x2(gf[j], vr[kk + j], pacc);
+            }
+        }
+        // Row statistics of rows acc_row(4g + 0..3, h32) = 8g + 4*h32 + 0..3.
+        f32x4 l2v[4], dlv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            l2v[g] = *(const f32x4 *)&st[8 * g + 4 * h32];
+            dlv[g] = *(const f32x4 *)&st[kBq + 8 * g + 4 * h32];
+        }
+        const bool need_mask = k.key_tail || (CAUSAL && k.n0w + kBkw - 1 > m0);
+        if (!need_mask) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2v[i >> 2][i & 3]));
+                sacc[i] = p;                                   // P[m][n]
+                pacc[i] = p * (pacc[i] - dlv[i >> 2][i & 3]);  // dS[m][n]
+            }
+        } else {
+            const int nl = k.n0w + l32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = acc_row(i, h32);
+                float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2v[i >> 2][i & 3]));
+                if (nl >= S || (CAUSAL && nl > m0 + r)) p = 0.0f;
+                sacc[i] = p;
+                pacc[i] = p * (pacc[i] - dlv[i >> 2][i & 3]);
+            }
+        }
+        const int bbase = 4 * h32 * L::QSTR + DB * l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int off = bbase + ((i >> 2) * 8 + (i & 3)) * L::QSTR;
+            const typename VecN<DB>::T gf = *(const typename VecN<DB>::T *)&gs[off];
+            const typename VecN<DB>::T qf = *(const typename VecN<DB>::T *)&qs[off];
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                dvacc[db] = mfma_32x32x2(sacc[i], vget<DB>(gf, db), dvacc[db]);
+                dkacc[db] = mfma_32x32x2(pacc[i], vget<DB>(qf, db), dkacc[db]);
+            }
+        }
+    } else {
+        pacc = zero16();  // no visible key: this wave's dS block is 0
+    }
+    // Every wave has finished the previous block's phase 2 (its reads of ds).
+    __syncthreads();
+    {
+        const int sbase = 4 * h32 * L::SSTR + kBkw * w + l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ds[sbase + ((i >> 2) * 8 + (i & 3)) * L::SSTR] = pacc[i];
+    }
+    wait_vmem();  // this wave's copies into (qn, gn, stn) have landed
+    __syncthreads();
+
+    // ---- phase 2: dQ[m0:m0+32, 32*dblk:+32] += scale * dS . K (this wave's keys) ----
+    const int dblk = w % DB;
+    const int nbase = (w / DB) * L::NK;
+    f32x16 qacc = zero16();
+    const int sa = l32 * L::SSTR + nbase + h32 * L::NKH;
+    const int kbase = (nbase + h32 * L::NKH) * D + (nbase / L::NKH + h32) * 32 + 32 * dblk + l32;
+#pragma unroll
+    for (int kk = 0; kk < L::NKH; kk += 4) {
+        const f32x4 sf = *(const f32x4 *)&ds[sa + kk];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qacc = mfma_32x32x2(sf[j], kall[kbase + (kk + j) * D], qacc);
+    }
+    // Row i of the block: wave-uniform row base + unsigned lane offset.
+    float *dqb = k.dqp + (int64_t)m0 * k.in_ss + 32 * dblk;
+    const unsigned qoff = (unsigned)(4 * h32 * k.in_ss + l32);
+    if (m0 + kBq <= S) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
+            unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
+            if (m0 + acc_row(i, h32) < S) unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
+        }
+    }
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
+{
+    typedef BwdLayout<D> L;
+    constexpr int DH = D / 2;
+    constexpr int DB = L::DB;
+    static_assert(L::SLOTS <= kMaxSlots, "copy slots");
+    __shared__ float Kall[L::KALL];
+    __shared__ float Qs0[L::QBUF], Qs1[L::QBUF];
+    __shared__ float dOs0[L::QBUF], dOs1[L::QBUF];
+    __shared__ float St0[2 * kBq], St1[2 * kBq];
+    __shared__ float dSs[kBq * L::SSTR];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+
+    const int BH = (int)(gridDim.x / a.nkb);
+    const int kb = blockIdx.x / BH;  // ascending: the longest causal rows first
+    const int bh = blockIdx.x - kb * BH;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int n0 = kb * kBk;
+
+    BwdBlock k;
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
+    k.qp = a.q + in_base;
+    k.gp = a.dout + out_base;
+    k.l2p = a.lse2 + (int64_t)bh * a.S_pad;
+    k.dlp = a.delta + (int64_t)bh * a.S_pad;
+    k.dqp = a.dq + in_base;
+    k.S = S;
+    k.nq = (S + kBq - 1) / kBq;
+    k.w = w;
+    k.n0w = n0 + kBkw * w;
+    k.in_ss = (int)a.in_ss;  // row strides < 2^24, checked on the host
+    k.out_ss = (int)a.out_ss;
+    k.key_tail = k.n0w + kBkw > S;
+#pragma unroll
+    for (int s = 0; s < kMaxSlots; ++s) {
+        const int p = 64 * (w + kWaves * s) + lane;
+        const int r = p / L::QROWCH;
+        const int c4 = p - r * L::QROWCH;
+        const bool real = p < L::QCHUNKS && c4 < D / 4;
+        k.qoff[s] = real ? r * k.in_ss + 4 * c4 : -1;
+        k.goff[s] = real ? r * k.out_ss + 4 * c4 : -1;
+        k.row[s] = real ? r : 0;
+    }
+
+    // Resident B operands: lane holds K[nl][h32*DH + kk] and V[nl][...].
+    float kr[DH], vr[DH];
+    {
+        const int nl = k.n0w + l32;
+        const int nrow = nl < S ? nl : S - 1;
+        const float *ks = a.k + in_base + (int64_t)nrow * a.in_ss + h32 * DH;
+        const float *vs = a.v + in_base + (int64_t)nrow * a.in_ss + h32 * DH;
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            const f32x4 t = *(const f32x4 *)(ks + kk);
+            const f32x4 u = *(const f32x4 *)(vs + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                kr[kk + j] = t[j];
+                vr[kk + j] = u[j];
+            }
+        }
+    }
+    // K tile of the whole workgroup into LDS (zeros past the sequence end).
+#pragma unroll
+    for (int it = 0; it < kBk * D / 4 / kThreads; ++it) {
+        const int idx = it * kThreads + tid;
+        const int r = idx / (D / 4);
+        const int c4 = idx - r * (D / 4);
+        const int n = n0 + r;
+        f32x4 kv = {0.f, 0.f, 0.f, 0.f};
+        if (n < S) kv = *(const f32x4 *)(a.k + in_base + (int64_t)n * a.in_ss + 4 * c4);
+        *(f32x4 *)&Kall[r * D + (r / L::NKH) * 32 + 4 * c4] = kv;
+    }
+
+    f32x16 dvacc[DB], dkacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        dvacc[db] = zero16();
+        dkacc[db] = zero16();
+    }
+
+    // First block into buffer set 0; afterwards every step copies the next
+    // block into the other set while it computes.
+    const int qstart = CAUSAL ? n0 / kBq : 0;
+    bwd_fetch<D>(k, qstart * kBq, Qs0, dOs0, St0);
+    wait_vmem();
+    __syncthreads();
+
+    for (int qb = qstart; qb < k.nq; qb += 2) {
+        bwd_step<D, CAUSAL>(a, k, qb, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1, Kall, kr, vr, dvacc,
+                            dkacc);
+        if (qb + 1 < k.nq)
+            bwd_step<D, CAUSAL>(a, k, qb + 1, Qs1, dOs1, St1, dSs, Qs0, dOs0, St0, Kall, kr, vr,
+                                dvacc, dkacc);
+    }
+
+    // dK (scaled) and dV rows of this wave's keys: register i -> key
+    // n0w + acc_row(i, h32), lane -> d = DB*l32 + db.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int n = k.n0w + acc_row(i, h32);
+        if (n >= S) continue;
+        float *dkrow = a.dk + in_base + (int64_t)n * a.in_ss + DB * l32;
+        float *dvrow = a.dv + in_base + (int64_t)n * a.in_ss + DB * l32;
+        typename VecN<DB>::T kout, vout;
+        if constexpr (DB == 1) {
+            kout = dkacc[0][i] * a.scale;
+            vout = dvacc[0][i];
+        } else {
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                kout[db] = dkacc[db][i] * a.scale;
+                vout[db] = dvacc[db][i];
+            }
+        }
+        *(typename VecN<DB>::T *)dkrow = kout;
+        *(typename VecN<DB>::T *)dvrow = vout;
+    }
+}
+
+template <int D, bool CAUSAL>
+int launch_bwd(const BwdArgs &args, int64_t rows_pad, int nblocks)
+{
+    constexpr int RPB = 256 / (D / 4);
+    const int pre_blocks = (int)((rows_pad + RPB - 1) / RPB);
+    hipLaunchKernelGGL((attn_bwd_pre<D>), dim3(pre_blocks), dim3(256), 0, 0, args, rows_pad);
+    if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
+    hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    return launch_ok("attn_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
+}  // namespace
+}  // namespace ember
+
