@@ -23,7 +23,7 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
     using namespace ember;
     const void *ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv};
     const int64_t strides[] = {in_sb, in_sh, in_ss, out_sb, out_sh, out_ss};
-    int st = check_attention_args(ptrs, 9, B, H, S, D, strides, 6, "attention_bwd");
+    int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, "attention_bwd");
     if (st != EMBER_OK || B * H * S == 0) return st;
 
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;

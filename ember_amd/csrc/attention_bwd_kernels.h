@@ -45,7 +45,8 @@
 namespace ember {
 
 int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t H, int64_t S,
-                         int64_t D, const int64_t *strides, int nstrides, const char *who);
+                         int64_t D, float scale, const int64_t *strides, int nstrides,
+                         const char *who);
 
 struct BwdArgs {
     const float *q, *k, *v, *o, *lse, *dout;

@@ -17,8 +17,9 @@
 //   and the row sum stays a per-lane partial until the end
 //   O^T (D x 32 queries) += V_tile^T . P^T      -- P^T straight from the S^T
 //                                                  accumulator registers
-// The softmax runs in base 2 with scale*log2(e) folded into one multiply;
-// LSE is stored in natural log.  Causal: tiles wholly above a wave's
+// The softmax runs in base 2 with scale*log2(e) folded into one FMA per
+// score, on v_exp_f32, with lazy rescaling of O (see the loop); LSE is
+// stored in natural log.  Causal: tiles wholly above a wave's
 // diagonal are skipped per wave, the mask (key <= query, integer compare) is
 // applied only on tiles that cross the diagonal or the sequence end.
 #include <math.h>
@@ -73,8 +74,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
 
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const float *__restrict__ qp = a.q + in_base;
-    const float *__restrict__ kp = a.k + in_base;
-    const float *__restrict__ vp = a.v + in_base;
 
     // Q^T operand: lane holds Q[mq][h32*DH + kk] for k-step kk.
     float qr[DH];
@@ -92,29 +91,50 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
     f32x16 oacc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[db] = zero16();
-    float mrun = -INFINITY;  // running max of s*c for query mq
+    float mrun = -INFINITY;  // reference max of s*c for query mq (see below)
     float lrun = 0.0f;       // this lane half's share of the running sum
 
     const int kend = CAUSAL ? min(S, q0 + kBr) : S;
     const int ntiles = (kend + kBc - 1) / kBc;
     constexpr int kLoads = kBc * D / 4 / kThreads;
+    const float *__restrict__ kp = a.k + in_base;
+    const float *__restrict__ vp = a.v + in_base;
 
     for (int t = 0; t < ntiles; ++t) {
+        // Per-lane offsets below derive from `tid`, which the empty asm makes
+        // opaque per tile, so that the compiler recomputes them (a few VALU
+        // ops) instead of hoisting them out of the loop and spilling.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
         const int n0 = t * kBc;
+        const float *kt = kp + (int64_t)n0 * a.in_ss;
+        const float *vt = vp + (int64_t)n0 * a.in_ss;
         __syncthreads();
+        if (n0 + kBc <= S) {
 #pragma unroll
-        for (int it = 0; it < kLoads; ++it) {
-            const int idx = it * kThreads + tid;
-            const int r = idx / (D / 4);
-            const int c4 = idx - r * (D / 4);
-            const int n = n0 + r;
-            f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-            if (n < S) {
-                kv = *(const f32x4 *)(kp + (int64_t)n * a.in_ss + 4 * c4);
-                vv = *(const f32x4 *)(vp + (int64_t)n * a.in_ss + 4 * c4);
+            for (int it = 0; it < kLoads; ++it) {
+                const int idx = it * kThreads + tid;
+                const int r = idx / (D / 4);
+                const int c4 = idx - r * (D / 4);
+                const unsigned off = (unsigned)(r * (int)a.in_ss + 4 * c4);
+                *(f32x4 *)&Ks[r * KSTR + 4 * c4] = *(const f32x4 *)(kt + off);
+                *(f32x4 *)&Vs[r * D + 4 * c4] = *(const f32x4 *)(vt + off);
             }
-            *(f32x4 *)&Ks[r * KSTR + 4 * c4] = kv;
-            *(f32x4 *)&Vs[r * D + 4 * c4] = vv;
+        } else {
+#pragma unroll
+            for (int it = 0; it < kLoads; ++it) {
+                const int idx = it * kThreads + tid;
+                const int r = idx / (D / 4);
+                const int c4 = idx - r * (D / 4);
+                f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+                if (n0 + r < S) {
+                    const unsigned off = (unsigned)(r * (int)a.in_ss + 4 * c4);
+                    kv = *(const f32x4 *)(kt + off);
+                    vv = *(const f32x4 *)(vt + off);
+                }
+                *(f32x4 *)&Ks[r * KSTR + 4 * c4] = kv;
+                *(f32x4 *)&Vs[r * D + 4 * c4] = vv;
+            }
         }
         __syncthreads();
         if (CAUSAL && n0 > m0 + 31) continue;  // tile wholly above this wave's diagonal
@@ -133,37 +153,59 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
             }
         }
 
-        // Scale, mask, tile max.
+        // Mask (diagonal and tail tiles only), tile max of the raw scores.
         const bool need_mask = (n0 + kBc > S) || (CAUSAL && n0 + kBc - 1 > m0);
-        float tmax = -INFINITY;
+        if (need_mask) {
 #pragma unroll
-        for (int blk = 0; blk < kBc / 32; ++blk) {
+            for (int blk = 0; blk < kBc / 32; ++blk) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float s = sacc[blk][i] * a.c;
-                if (need_mask) {
+                for (int i = 0; i < 16; ++i) {
                     const int n = n0 + 32 * blk + acc_row(i, h32);
-                    if (n >= S || (CAUSAL && n > mq)) s = -INFINITY;
+                    const bool vis = (n < S) & (!CAUSAL | (n <= mq));
+                    sacc[blk][i] = vis ? sacc[blk][i] : -INFINITY;
                 }
-                sacc[blk][i] = s;
-                tmax = fmaxf(tmax, s);
             }
         }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < kBc / 32; ++blk)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[blk][i]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        // Tile 0 always holds key 0, visible to every query, so mnew is finite.
-        const float mnew = fmaxf(mrun, tmax);
-        const float alpha = exp2f(mrun - mnew);
-        mrun = mnew;
-        lrun *= alpha;
+        // Scaled tile max (scale >= 0, checked on the host).  The reference
+        // max mrun is raised only when some lane's scores would otherwise
+        // exceed it by more than 2^8 (lazy rescaling): the result is the same
+        // softmax, and most tiles skip the rescale of O.  Tile 0 holds key 0,
+        // visible to every query, so it always sets a finite mrun.
+        const float tm2 = tmax * a.c;
+        if (__ballot(tm2 > mrun + 8.0f) != 0) {
+            const float mnew = fmaxf(mrun, tm2);
+            const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+            mrun = mnew;
+            lrun *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+            for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+        }
+        if (need_mask) {
 #pragma unroll
-        for (int blk = 0; blk < kBc / 32; ++blk) {
+            for (int blk = 0; blk < kBc / 32; ++blk) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = exp2f(sacc[blk][i] - mnew);
-                sacc[blk][i] = p;
-                lrun += p;
+                for (int i = 0; i < 16; ++i) {
+                    const float sv = sacc[blk][i];
+                    const float p = sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv, a.c, -mrun));
+                    sacc[blk][i] = p;
+                    lrun += p;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(sacc[blk][i], a.c, -mrun));
+                    sacc[blk][i] = p;
+                    lrun += p;
+                }
             }
         }
 
@@ -212,9 +254,10 @@ int launch_fwd(const FwdArgs &args, int nblocks)
 
 // Shared argument checks for attention_fwd / attention_bwd.
 int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t H, int64_t S,
-                         int64_t D, const int64_t *strides, int nstrides, const char *who)
+                         int64_t D, float scale, const int64_t *strides, int nstrides,
+                         const char *who)
 {
-    if (B < 0 || H < 0 || S < 0 || D <= 0)
+    if (B < 0 || H < 0 || S < 0 || D <= 0 || !(scale >= 0.0f) || isinf(scale))
         return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     if (D != 32 && D != 64 && D != 128) return record_error(EMBER_ERR_UNSUPPORTED, who);
     if (S > (int64_t)INT32_MAX / 2 || B * H > (int64_t)INT32_MAX / 1024)
@@ -240,7 +283,7 @@ extern "C" int attention_fwd(const float *q, const float *k, const float *v, flo
     using namespace ember;
     const void *ptrs[] = {q, k, v, o, lse};
     const int64_t strides[] = {in_sb, in_sh, in_ss, out_sb, out_sh, out_ss};
-    int st = check_attention_args(ptrs, 5, B, H, S, D, strides, 6, "attention_fwd");
+    int st = check_attention_args(ptrs, 5, B, H, S, D, scale, strides, 6, "attention_fwd");
     if (st != EMBER_OK || B * H * S == 0) return st;
 
     FwdArgs args;
