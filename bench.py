@@ -120,6 +120,70 @@ def cpu_baseline(S, D, threads):
     }
 
 
+def _timed(ev, fn, reps):
+    """Average ms of fn() over reps launches, HIP events on the null stream."""
+    fn()
+    marks = ev.create(reps + 1)
+    ev.record(marks[0])
+    for i in range(reps):
+        fn()
+        ev.record(marks[i + 1])
+    return sum(ev.elapsed_ms(marks[i], marks[i + 1]) for i in range(reps)) / reps
+
+
+def secondary(L, ev):
+    """The other BASELINE configs, measured the same way (reported beside the
+    headline, not part of `value`): attention fwd at configs 1 and 2, the
+    attention part of config 5 (fwd+bwd), the config-4 GEMM shapes, and the
+    forward at short S where it is HBM-bound (achieved GB/s)."""
+    out = {}
+    rng = np.random.default_rng(5)
+
+    def attn(tag, B, H, S, D, causal, bwd, reps):
+        n = B * H * S * D
+        host = rng.standard_normal(n, dtype=np.float32)
+        q, k, v = (DeviceArray((n,), host) for _ in range(3))
+        g = DeviceArray((n,), host) if bwd else None
+        o, lse = DeviceArray((n,)), DeviceArray((B * H * S,))
+        dq, dk, dv = (DeviceArray((n,)) for _ in range(3)) if bwd else (None, None, None)
+        st = capi.contiguous_strides(B, H, S, D)
+        sc = float(np.float32(1.0 / math.sqrt(D)))
+        f = lambda: L.attention_fwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, B, H, S, D, sc,
+                                    int(causal), *st, *st)  # noqa: E731
+        fwd_fl, bwd_fl = attention_flops(B, H, S, D, causal)
+        fwd_ms = _timed(ev, f, reps)
+        rec = {"shape": f"B{B} H{H} S{S} D{D} causal={causal}", "fwd_ms": round(fwd_ms, 4),
+               "fwd_tflops": round(fwd_fl / fwd_ms / 1e9, 2)}
+        if bwd:
+            b = lambda: L.attention_bwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, g.ptr, dq.ptr,  # noqa: E731
+                                        dk.ptr, dv.ptr, B, H, S, D, sc, int(causal), *st, *st)
+            bwd_ms = _timed(ev, b, reps)
+            rec.update(bwd_ms=round(bwd_ms, 4), bwd_tflops=round(bwd_fl / bwd_ms / 1e9, 2),
+                       fwd_bwd_tflops=round((fwd_fl + bwd_fl) / (fwd_ms + bwd_ms) / 1e9, 2))
+        fwd_bytes = 16 * B * H * S * D + 4 * B * H * S
+        rec["fwd_hbm_gbs"] = round(fwd_bytes / fwd_ms / 1e6, 1)
+        capi.check(what=tag)
+        out[tag] = rec
+
+    attn("config1_fwd", 1, 4, 256, 64, False, False, 50)
+    attn("config2_causal_fwd", 8, 16, 2048, 64, True, False, 20)
+    attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20)
+    for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
+        attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
+
+    for tag, (n, k, m) in {"config4_gemm_4096": (4096, 4096, 4096),
+                           "config4_gemm_16384x1024x3072": (16384, 1024, 3072)}.items():
+        a = DeviceArray((n * k,), rng.uniform(-1, 1, n * k).astype(np.float32))
+        b = DeviceArray((k * m,), rng.uniform(-1, 1, k * m).astype(np.float32))
+        c = DeviceArray((n * m,))
+        ms = _timed(ev, lambda: L.matmul(a.ptr, b.ptr, c.ptr, n, m, k), 10)
+        capi.check(what=tag)
+        out[tag] = {"shape": f"n={n} k={k} m={m}", "ms": round(ms, 4),
+                    "tflops": round(2.0 * n * m * k / ms / 1e9, 2),
+                    "frac_of_fp32_mfma_peak": round(2.0 * n * m * k / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS, 4)}
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,6 +194,8 @@ def main(argv=None):
     ap.add_argument("--seq", type=int, default=4096)
     ap.add_argument("--head-dim", type=int, default=128)
     ap.add_argument("--non-causal", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other configs (1, 2, 4, 5-attention, short S)")
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="host threads (= heads) for the CPU baseline; 0 skips it")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -248,6 +314,9 @@ def main(argv=None):
         L.sync_device()
         capi.check(what="copy probe")
         result["copy_probe_bytes"] = {"read": 4 * n, "write": 4 * n}
+
+    if not args.no_secondary:
+        result["secondary"] = secondary(L, ev)
 
     threads = args.cpu_threads
     if threads is None:
