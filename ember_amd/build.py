@@ -90,8 +90,6 @@ def build_library(extra_flags: list[str] | None = None) -> str:
 
 def build_extensions() -> list[str]:
     inc_py = sysconfig.get_paths()["include"]
-    import numpy
-
     suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
     built = []
     for mod, srcs in EXTENSIONS:
@@ -103,7 +101,8 @@ def build_extensions() -> list[str]:
         rel = os.path.relpath(PKG, os.path.dirname(out))
         _run([
             "gcc", "-O2", "-std=gnu11", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
-            "-I", inc_py, "-I", numpy.get_include(), "-I", os.path.join(ROOT, "include"),
+            "-Wno-missing-field-initializers",
+            "-I", inc_py, "-I", os.path.join(ROOT, "include"), "-I", CSRC,
             *srcs, "-o", out + ".tmp",
             "-L", PKG, "-lember_amd", f"-Wl,-rpath,$ORIGIN/{rel}",
         ])
