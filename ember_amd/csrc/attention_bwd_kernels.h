@@ -40,6 +40,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "lds_dma.h"
 #include "mfma.h"
 
 namespace ember {
@@ -103,23 +104,6 @@ __global__ __launch_bounds__(256) void attn_bwd_pre(BwdArgs a, int64_t rows_pad)
     }
     const int64_t qoff = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub;
     *(f32x4 *)(a.dq + qoff) = f32x4{0.f, 0.f, 0.f, 0.f};
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l's data
-// lands at lds + 16*l bytes (gfx950 global_load_lds_dwordx4; lds must be
-// wave-uniform).
-__device__ __forceinline__ void dma16(const float *src, float *lds)
-{
-    typedef __attribute__((address_space(1))) void gvoid;
-    typedef __attribute__((address_space(3))) void lvoid;
-    __builtin_amdgcn_global_load_lds((gvoid *)src, (lvoid *)lds, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(0): every vector-memory operation this wave issued,
-// including LDS-bound copies, has completed.
-__device__ __forceinline__ void wait_vmem()
-{
-    __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 template <int D>

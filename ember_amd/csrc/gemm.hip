@@ -19,6 +19,7 @@
 // so the two lane halves read disjoint banks.  Workgroups are ordered so
 // that consecutive ones share B column panels in L2.
 #include "common.h"
+#include "lds_dma.h"
 #include "mfma.h"
 
 namespace ember {
@@ -183,6 +184,138 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(GemmArgs g)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Fast path for tile-aligned shapes (n % 128 == 0, m % 256 == 0, k % 16 == 0,
+// 16-byte aligned operands): 128 x 256 block of out per workgroup, 64 x 128
+// per wave as 2 x 4 accumulators, two workgroups per CU.
+//   * k is walked in slabs of 16, copied HBM -> LDS directly
+//     (global_load_lds_dwordx4, no registers) one slab ahead into the
+//     other of two buffers; one barrier per slab.
+//   * A slab (128 x 16) sits in rows padded to 20 floats: the A operand
+//     (16 rows at one column per lane group) then hits 16 different bank
+//     groups.  B slab (16 x 256) is unpadded: a lane reads 4 consecutive
+//     columns with one ds_read_b128, one per accumulator column block
+//     (column = 4*lane + cb), so each B read feeds 8 MFMAs and each A read 16.
+//   * every LDS address in the loop is a per-lane base plus a compile-time
+//     offset.
+//   * tiles are numbered so that the tiles one XCD runs (workgroup ids are
+//     dealt to the 8 XCDs round-robin) are contiguous, and within that
+//     range grouped 8 row tiles per B column panel for L2 reuse.
+constexpr int FM = 128, FN = 256, FK = 16;
+constexpr int FASTR = FK + 4;                 // padded A row
+constexpr int FA_CHUNKS = FM * (FASTR / 4);   // 16-byte chunks per A slab (640)
+constexpr int FA_DMA = FA_CHUNKS / 64;        // 1 KiB copies per A slab (10)
+constexpr int FB_DMA = FK;                    // one 1 KiB copy per B row (16)
+constexpr int FA_BUF = FM * FASTR;            // floats
+constexpr int FB_BUF = FK * FN;
+
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
+{
+    __shared__ float As0[FA_BUF], As1[FA_BUF];
+    __shared__ float Bs0[FB_BUF], Bs1[FB_BUF];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    const int wr = w >> 1, wc = w & 1;
+
+    const int ntiles = g.tiles_n * g.tiles_m;
+    int tile = blockIdx.x;
+    if (ntiles % 8 == 0) tile = (tile % 8) * (ntiles / 8) + tile / 8;
+    constexpr int GROUP = 8;
+    const int per_group = GROUP * g.tiles_m;
+    const int grp = tile / per_group;
+    const int first = grp * GROUP;
+    const int rows_in_grp = min(GROUP, g.tiles_n - first);
+    const int in_grp = tile - grp * per_group;
+    const int row0 = (first + in_grp % rows_in_grp) * FM;
+    const int col0 = (in_grp / rows_in_grp) * FN;
+    const float *A = g.a + (int64_t)blockIdx.y * g.sa + (int64_t)row0 * g.k;
+    const float *B = g.b + (int64_t)blockIdx.y * g.sb + col0;
+    float *C = g.c + (int64_t)blockIdx.y * g.sc + (int64_t)row0 * g.m + col0;
+
+    // This lane's chunk of each A copy it issues (t = w, w+4, w+8 < 10):
+    // row p / 5, chunk p % 5 (chunk 4 is row padding: re-read chunk 0).
+    unsigned aoff[3];
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+        const int p = 64 * (w + 4 * s) + lane;
+        const int r = p / (FASTR / 4);
+        const int c = p - r * (FASTR / 4);
+        aoff[s] = (unsigned)(r * g.k + 4 * (c < 4 ? c : 0));
+    }
+    const unsigned boff = (unsigned)(4 * lane);
+
+    auto fetch = [&](int k0, float *__restrict__ as, float *__restrict__ bs) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+            if (w + 4 * s < FA_DMA) dma16(A + k0 + aoff[s], as + 256 * (w + 4 * s));
+#pragma unroll
+        for (int s = 0; s < FB_DMA / 4; ++s) {
+            const int r = w + 4 * s;
+            dma16(B + (int64_t)(k0 + r) * g.m + boff, bs + 256 * r);
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
+
+    const int abase = (64 * wr + l32) * FASTR + 8 * h32;
+    const int bbase = 8 * h32 * FN + 128 * wc + 4 * l32;
+    auto slab = [&](const float *__restrict__ as, const float *__restrict__ bs) {
+#pragma unroll
+        for (int kk = 0; kk < 8; kk += 4) {
+            f32x4 af[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) af[rb] = *(const f32x4 *)&as[abase + rb * 32 * FASTR + kk];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 bf = *(const f32x4 *)&bs[bbase + (kk + j) * FN];
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_32x32x2(af[rb][j], bf[cb], acc[rb][cb]);
+            }
+        }
+    };
+
+    const int nslab = g.k / FK;
+    fetch(0, As0, Bs0);
+    wait_vmem();
+    __syncthreads();
+    // Two slabs per trip so that each buffer is a distinct LDS object: the
+    // compiler then knows the copy into one does not feed reads of the other.
+    for (int s = 0; s < nslab; s += 2) {
+        if (s + 1 < nslab) fetch((s + 1) * FK, As1, Bs1);
+        slab(As0, Bs0);
+        wait_vmem();
+        __syncthreads();
+        if (s + 1 < nslab) {
+            if (s + 2 < nslab) fetch((s + 2) * FK, As0, Bs0);
+            slab(As1, Bs1);
+            wait_vmem();
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = 64 * wr + 32 * rb + acc_row(i, h32);
+            f32x4 v;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) v[cb] = acc[rb][cb][i];
+            *(f32x4 *)&C[(int64_t)row * g.m + 128 * wc + 4 * l32] = v;
+        }
+    }
+}
+
 void gemm_launch(const float *a, const float *b, float *out, int batch, int n, int m, int k,
                  const char *who)
 {
@@ -208,6 +341,14 @@ void gemm_launch(const float *a, const float *b, float *out, int batch, int n, i
         return;
     }
     const bool vec = (k % 4 == 0) && (m % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
+    if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 && ((uintptr_t)out % 16) == 0) {
+        g.tiles_n = n / FM;
+        g.tiles_m = m / FN;
+        hipLaunchKernelGGL(gemm_f32_dma_kernel, dim3(g.tiles_n * g.tiles_m, batch), dim3(kThreads),
+                           0, 0, g);
+        launch_ok(who);
+        return;
+    }
     const dim3 grid(g.tiles_n * g.tiles_m, batch);
     if (vec)
         hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(kThreads), 0, 0, g);

@@ -1,0 +1,34 @@
+// lds_dma.h -- direct HBM -> LDS copies on gfx950 (not part of the public ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace ember {
+
+// 16 bytes per lane from global memory straight into LDS, bypassing
+// registers: lane l's data lands at lds + 16*l bytes
+// (global_load_lds_dwordx4; `lds` must be wave-uniform).  Completion is
+// tracked by the wave's vmcnt like any vector-memory load.
+__device__ __forceinline__ void dma16(const float *src, float *lds)
+{
+    typedef __attribute__((address_space(1))) void gvoid;
+    typedef __attribute__((address_space(3))) void lvoid;
+    __builtin_amdgcn_global_load_lds((gvoid *)src, (lvoid *)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// and lgkmcnt left at their maxima): at most N of this wave's vector-memory
+// operations, including LDS-bound copies, are still in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmem_n()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ void wait_vmem()
+{
+    wait_vmem_n<0>();
+}
+
+}  // namespace ember

@@ -50,23 +50,29 @@ def test_reference_batched_cases(shape_a, shape_b):
     "n,k,m",
     [(32, 128, 64), (1, 10, 5), (64, 32, 128), (16, 50, 50),        # test_linear.py shapes
      (127, 33, 129), (128, 32, 128), (129, 1, 255), (257, 300, 3), (5, 4096, 7),
-     (300, 64, 260), (1000, 500, 700)],
+     (300, 64, 260), (1000, 500, 700),
+     # tile-aligned shapes (n % 128, m % 256, k % 16 == 0) take the LDS-DMA kernel
+     (128, 16, 256), (256, 48, 512), (384, 1024, 768), (1024, 16, 2048)],
 )
 def test_matmul_within_fp32_bound(n, k, m):
     a, b = _u((n, k), n), _u((k, m), m)
     _check(G.matmul(a, b), a, b)
 
 
-def test_batched_matches_per_batch():
-    a, b = _u((5, 130, 70), 3), _u((5, 70, 90), 4)
+@pytest.mark.parametrize("shape_a, shape_b", [((5, 130, 70), (5, 70, 90)),
+                                              ((3, 128, 32), (3, 32, 256))])
+def test_batched_matches_per_batch(shape_a, shape_b):
+    a, b = _u(shape_a, 3), _u(shape_b, 4)
     got = G.matmul_batched(a, b)
-    for i in range(5):
+    for i in range(shape_a[0]):
         _check(got[i], a[i], b[i])
 
 
 def test_identity_and_integers_are_exact():
     a = _u((200, 136), 5)
     assert np.array_equal(G.matmul(a, np.eye(136, dtype=np.float32)), a)
+    a = _u((256, 512), 6)   # tile-aligned: the LDS-DMA kernel
+    assert np.array_equal(G.matmul(a, np.eye(512, dtype=np.float32)), a)
     rng = np.random.default_rng(6)
     ai = rng.integers(-8, 8, (150, 260)).astype(np.float32)
     bi = rng.integers(-8, 8, (260, 90)).astype(np.float32)
