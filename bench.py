@@ -171,6 +171,27 @@ def secondary(L, ev):
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
 
+    # Fused Adam over config 5's parameters (pre-LN decoder block, d=1024,
+    # MLP 4x): LN gains/biases, QKV, out-proj, MLP weights and biases.
+    d = 1024
+    shapes = [d, d, 3 * d * d, 3 * d, d * d, d, d, d, 4 * d * d, 4 * d, 4 * d * d, d]
+    tens = [[DeviceArray((n,), rng.standard_normal(n).astype(np.float32)) for _ in range(4)]
+            for n in shapes]
+    nparam = sum(shapes)
+    t_box = [0]
+
+    def adam():
+        t_box[0] += 1
+        return capi.adam_step([x[0] for x in tens], [x[1] for x in tens], [x[2] for x in tens],
+                              [x[3] for x in tens], 1e-3, 0.9, 0.999, 1e-8, t_box[0])
+
+    ms = _timed(ev, adam, 20)
+    capi.check(what="adam_step")
+    out["config5_fused_adam"] = {"params": nparam, "tensors": len(shapes), "ms": round(ms, 4),
+                                 "hbm_gbs": round(28.0 * nparam / ms / 1e6, 1),
+                                 "frac_of_hbm_peak": round(28.0 * nparam / ms / 1e6 / PEAK_HBM_GBS, 4)}
+    del tens
+
     for tag, (n, k, m) in {"config4_gemm_4096": (4096, 4096, 4096),
                            "config4_gemm_16384x1024x3072": (16384, 1024, 3072)}.items():
         a = DeviceArray((n * k,), rng.uniform(-1, 1, n * k).astype(np.float32))

@@ -8,6 +8,7 @@ from ._em_random import _constant, _seed, _uniform
 from ._tensor import (
     _add_broadcasted,
     _add_scalar,
+    _adam_step,
     _add_tensor,
     _attention_bwd,
     _attention_fwd,
@@ -68,4 +69,4 @@ REFERENCE_NAMES = (
     "_Tensor", "_transpose", "_truediv_broadcasted", "_truediv_scalar", "_truediv_tensor",
 )
 
-__all__ = list(REFERENCE_NAMES) + ["_attention_fwd", "_attention_bwd", "_synchronize"]
+__all__ = list(REFERENCE_NAMES) + ["_attention_fwd", "_attention_bwd", "_adam_step", "_synchronize"]

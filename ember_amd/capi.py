@@ -73,6 +73,8 @@ def lib() -> C.CDLL:
     L.attention_fwd.argtypes = [_vp] * 5 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
     L.attention_bwd.restype = C.c_int
     L.attention_bwd.argtypes = [_vp] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
+    L.adam_step.restype = C.c_int
+    L.adam_step.argtypes = [C.POINTER(_vp)] * 4 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 4 + [_i64]
     _lib = L
     return L
 
@@ -132,3 +134,12 @@ class DeviceArray:
 def contiguous_strides(B: int, H: int, S: int, D: int) -> tuple[int, int, int]:
     """(stride_b, stride_h, stride_s) of a dense (B, H, S, D) tensor."""
     return (H * S * D, S * D, D)
+
+
+def adam_step(params, grads, means, variances, lr, beta1, beta2, eps, step) -> int:
+    """adam_step over lists of DeviceArray (same lengths and sizes)."""
+    n = len(params)
+    table = lambda xs: (_vp * n)(*(x.ptr for x in xs))  # noqa: E731
+    sizes = (_i64 * n)(*(x.size for x in params))
+    return lib().adam_step(table(params), table(grads), table(means), table(variances), sizes, n,
+                           lr, beta1, beta2, eps, step)

@@ -117,6 +117,23 @@ int attention_bwd(const float *q, const float *k, const float *v, const float *o
                   int64_t in_sb, int64_t in_sh, int64_t in_ss,
                   int64_t out_sb, int64_t out_sh, int64_t out_ss);
 
+/* ---- fused Adam: replaces ember/optim/adam.py:24-45 (Adam.apply) ----
+ *
+ * One Adam step over `ntensors` parameter tensors in as few launches as
+ * possible (48 tensors per launch).  params[i], grads[i], exp_avg[i] (m),
+ * exp_avg_sq[i] (v) are device pointers to sizes[i] floats each; the
+ * pointer and size tables themselves are host memory.  p, m, v are updated
+ * in place.  The arithmetic is Ember's, operation by operation:
+ *   m = m*b1 + g*(1-b1);  v = v*b2 + (g*g)*(1-b2);
+ *   p = p - ((m/(1-b1^t))*lr) / (sqrt(v/(1-b2^t)) + eps)
+ * each step an fp32 operation rounded on its own (no fused multiply-add),
+ * with every scalar formed in double and rounded to fp32 once, so the result
+ * is bit-identical to the reference's composed element-wise operators.
+ * `step` (t) starts at 1.  Returns a status; argument errors launch nothing. */
+int adam_step(float *const *params, const float *const *grads, float *const *exp_avg,
+              float *const *exp_avg_sq, const int64_t *sizes, int ntensors, double lr,
+              double beta1, double beta2, double eps, int64_t step);
+
 #undef EMBER_BINARY_OP
 #undef EMBER_SCALAR_OP
 #undef EMBER_BROADCAST_OP

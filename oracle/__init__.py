@@ -61,6 +61,7 @@ def lib() -> C.CDLL:
         L.oracle_attention_fwd.restype = C.c_int
         L.oracle_attention_bwd.argtypes = [_f32p] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
         L.oracle_attention_bwd.restype = C.c_int
+        L.oracle_adam_step.argtypes = [_f32p] * 4 + [_i64] + [C.c_double] * 4 + [_i64]
         _lib = L
     return _lib
 
@@ -81,11 +82,12 @@ def ref_lib() -> C.CDLL:
         L.transpose.argtypes = [_f32p, _f32p, C.c_int, C.c_int]
         for name in ("sum_axis", "max_axis"):
             getattr(L, name).argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int]
-        for name in ("add_tensor", "sub_tensor", "mul_tensor"):
+        for name in ("add_tensor", "sub_tensor", "mul_tensor", "truediv_tensor"):
             getattr(L, name).argtypes = [_f32p, _f32p, _f32p, C.c_int]
-        for name in ("mul_scalar", "add_scalar"):
+        for name in ("mul_scalar", "add_scalar", "truediv_scalar"):
             getattr(L, name).argtypes = [_f32p, C.c_float, _f32p, C.c_int]
-        L.exponent_tensor.argtypes = [_f32p, _f32p, C.c_int]
+        for name in ("exponent_tensor", "sqrt_tensor"):
+            getattr(L, name).argtypes = [_f32p, _f32p, C.c_int]
         for name in ("sub_broadcasted", "truediv_broadcasted", "mul_broadcasted"):
             getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _i32p, _i32p, _i32p, C.c_int]
         _ref = L
@@ -246,3 +248,50 @@ def ref_composed_attention_head(qh, kh, vh, doh, causal: bool, scale: float, bac
     dk = np.empty_like(dk0)
     R.mul_scalar(dk0, np.float32(scale), dk, S * D)
     return o, dq, dk, dv
+
+
+# ------------------------------------------------------------------ Adam
+
+
+def adam_step(p, g, m, v, lr, beta1, beta2, eps, t):
+    """In-place Adam step on float32 arrays p, m, v with gradient g, the way
+    Ember's Adam.apply computes it (ember/optim/adam.py:24-45)."""
+    for x in (p, g, m, v):
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().oracle_adam_step(p, g, m, v, p.size, lr, beta1, beta2, eps, t)
+
+
+def ref_composed_adam_step(p, g, m, v, lr, beta1, beta2, eps, t):
+    """Returns (p, m, v) after one step run through the reference's own CPU
+    operators in adam.py's order; each Python scalar is rounded to float32
+    as the binding's "f" conversion does."""
+    R = ref_lib()
+    n = p.size
+    f32 = np.float32
+
+    def new():
+        return np.empty(n, dtype=np.float32)
+
+    def scal(fn, a, x):
+        out = new()
+        getattr(R, fn)(a, f32(x), out, n)
+        return out
+
+    def ten(fn, a, b):
+        out = new()
+        getattr(R, fn)(a, b, out, n)
+        return out
+
+    p, g, m, v = (np.ascontiguousarray(x, dtype=np.float32).reshape(-1) for x in (p, g, m, v))
+    m = scal("mul_scalar", m, beta1)                                      # m *= beta1
+    m = ten("add_tensor", m, scal("mul_scalar", g, 1 - beta1))            # m += (1-b1)*g
+    v = scal("mul_scalar", v, beta2)                                      # v *= beta2
+    v = ten("add_tensor", v, scal("mul_scalar", ten("mul_tensor", g, g), 1 - beta2))
+    m_hat = scal("truediv_scalar", m, 1 - beta1 ** t)
+    v_hat = scal("truediv_scalar", v, 1 - beta2 ** t)
+    num = scal("mul_scalar", m_hat, lr)                                   # lr * m_hat
+    sq = new()
+    R.sqrt_tensor(v_hat, sq, n)
+    den = scal("add_scalar", sq, eps)                                     # sqrt(v_hat) + eps
+    p = ten("sub_tensor", p, ten("truediv_tensor", num, den))             # p -= num / den
+    return p, m, v

@@ -194,3 +194,35 @@ int oracle_attention_bwd(const float *q, const float *k, const float *v, const f
     }
     return 0;
 }
+
+/* ---- Adam: restates ember/optim/adam.py:24-45 as Ember executes it ----
+ * Every line of adam.py is one fp32 element-wise operator of the reference
+ * (src/tensor/operators_cpu.c:8-44 via tensor_api.c), each rounded to fp32;
+ * the Python scalars are formed in double and converted to float by the
+ * binding ("f", tensor_api.c:213).  Built with -ffp-contract=off, so no
+ * multiply-add is fused.  In place on p, m, v. */
+void oracle_adam_step(float *p, const float *g, float *m, float *v, int64_t n, double lr,
+                      double beta1, double beta2, double eps, int64_t t)
+{
+    const float b1 = (float)beta1, omb1 = (float)(1.0 - beta1);
+    const float b2 = (float)beta2, omb2 = (float)(1.0 - beta2);
+    const float bc1 = (float)(1.0 - pow(beta1, (double)t));
+    const float bc2 = (float)(1.0 - pow(beta2, (double)t));
+    const float flr = (float)lr, feps = (float)eps;
+    for (int64_t i = 0; i < n; i++) {
+        float mi = m[i] * b1;                 /* m *= beta1                      */
+        const float gm = g[i] * omb1;         /* (1 - beta1) * g                 */
+        mi = mi + gm;                         /* m += ...                        */
+        float vi = v[i] * b2;                 /* v *= beta2                      */
+        const float gg = g[i] * g[i];         /* g * g                           */
+        const float gv = gg * omb2;           /* (1 - beta2) * (g * g)           */
+        vi = vi + gv;                         /* v += ...                        */
+        const float mh = mi / bc1;            /* m_hat                           */
+        const float vhat = vi / bc2;          /* v_hat                           */
+        const float num = mh * flr;           /* lr * m_hat                      */
+        const float den = sqrtf(vhat) + feps; /* sqrt(v_hat) + eps               */
+        p[i] = p[i] - num / den;              /* p -= num / den                  */
+        m[i] = mi;
+        v[i] = vi;
+    }
+}

@@ -217,3 +217,59 @@ def test_oracle_strided_layout_matches_contiguous():
     assert rc == 0
     assert np.array_equal(o.transpose(0, 2, 1, 3), o_ref)
     assert np.array_equal(lse, lse_ref)
+
+
+# ------------------------------------------------------------------- Adam
+
+
+def _adam_state(n, seed):
+    rng = np.random.default_rng(seed)
+    p = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    m = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    v = np.abs(0.01 * rng.standard_normal(n)).astype(np.float32)
+    return p, g, m, v
+
+
+@needs_ref
+@pytest.mark.parametrize("hp", [(1e-3, 0.9, 0.999, 1e-8), (0.01, 0.8, 0.99, 1e-6), (0.1, 0.5, 0.9, 1e-3)])
+@pytest.mark.parametrize("t", [1, 2, 17])
+def test_oracle_adam_is_bitwise_the_reference_composition(hp, t):
+    """oracle_adam_step == adam.py's 14 element-wise ops run through the
+    reference's own compiled operators_cpu.c, bit for bit."""
+    lr, b1, b2, eps = hp
+    p, g, m, v = _adam_state(1000, t)
+    rp, rm, rv = oracle.ref_composed_adam_step(p, g, m, v, lr, b1, b2, eps, t)
+    oracle.adam_step(p, g, m, v, lr, b1, b2, eps, t)
+    assert np.array_equal(p, rp) and np.array_equal(m, rm) and np.array_equal(v, rv)
+
+
+def test_oracle_adam_matches_the_textbook_formula():
+    """The reference's own test formula (tests/optim/test_adam.py:9-20), float64."""
+    lr, b1, b2, eps = 0.01, 0.9, 0.999, 1e-8
+    p, g, m, v = _adam_state(500, 3)
+    P, G, M, V = (x.astype(np.float64) for x in (p, g, m, v))
+    for t in (1, 2, 3):
+        M = b1 * M + (1 - b1) * G
+        V = b2 * V + (1 - b2) * G * G
+        P = P - lr * (M / (1 - b1 ** t)) / (np.sqrt(V / (1 - b2 ** t)) + eps)
+        oracle.adam_step(p, g, m, v, lr, b1, b2, eps, t)
+    # fp32 against float64: rtol as the reference's test, plus a small atol
+    # for entries that cancel to near zero.
+    np.testing.assert_allclose(p, P, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(m, M, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(v, V, rtol=1e-5, atol=1e-9)
+
+
+def test_oracle_adam_planted_mistakes_fail():
+    """Swapping the betas or dropping the bias correction must not pass."""
+    lr, b1, b2, eps = 0.01, 0.9, 0.999, 1e-8
+    base = _adam_state(200, 4)
+    good = [x.copy() for x in base]
+    oracle.adam_step(*good, lr, b1, b2, eps, 1)
+    bad = [x.copy() for x in base]
+    oracle.adam_step(*bad, lr, b2, b1, eps, 1)
+    assert not np.allclose(bad[0], good[0], rtol=1e-6)
+    bad = [x.copy() for x in base]
+    oracle.adam_step(*bad, lr, b1, b2, eps, 1000)   # bias corrections ~1
+    assert not np.allclose(bad[0], good[0], rtol=1e-6)
