@@ -131,6 +131,42 @@ def _timed(ev, fn, reps):
     return sum(ev.elapsed_ms(marks[i], marks[i + 1]) for i in range(reps)) / reps
 
 
+def decoder_step(B, S, d, H, steps):
+    """Times config 5's training step; flops as SURVEY 8(d): 3 x the forward
+    GEMMs (2*B*S*d*d*(3 + 1 + 4 + 4)) plus causal attention fwd+bwd."""
+    from ember_amd import Tensor, loss, nn, optim, random as erand
+
+    erand.seed(0)
+    block = nn.DecoderBlock(d, H, 4, True)
+    opt = optim.Adam(block.parameters(), lr=1e-3)
+    mse = loss.MSELoss()
+    rng = np.random.default_rng(6)
+    x = Tensor(rng.standard_normal((B * S, d), dtype=np.float32))
+    target = Tensor(rng.standard_normal((B * S, d), dtype=np.float32))
+
+    def step():
+        y = block(x, B, S)
+        value = mse(y, target)
+        block.backward(mse.backward())
+        opt.apply(block.gradients())
+        return value
+
+    first = step()
+    L = capi.lib()
+    L.sync_device()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        last = step()
+    L.sync_device()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    gemm = 3 * 2.0 * B * S * d * d * 12
+    fwd, bwd = attention_flops(B, H, S, d // H, True)
+    flops = gemm + fwd + bwd
+    return {"shape": f"B{B} S{S} d{d} H{H} mlp4x causal", "ms_per_step": round(ms, 3),
+            "tflops": round(flops / ms / 1e9, 2), "flops_per_step": flops,
+            "loss_first": round(float(first), 5), "loss_last": round(float(last), 5)}
+
+
 def secondary(L, ev):
     """The other BASELINE configs, measured the same way (reported beside the
     headline, not part of `value`): attention fwd at configs 1 and 2, the
@@ -191,6 +227,12 @@ def secondary(L, ev):
                                  "hbm_gbs": round(28.0 * nparam / ms / 1e6, 1),
                                  "frac_of_hbm_peak": round(28.0 * nparam / ms / 1e6 / PEAK_HBM_GBS, 4)}
     del tens
+
+    # Config 5: one decoder-block training step (forward, MSE loss, backward,
+    # fused Adam) at d=1024, 16 heads of 64, S=1024, B=8, causal, through the
+    # Python front-end.  Wall-clock per step (the loss is read back each step,
+    # as Ember's MSELoss returns a float).
+    out["config5_decoder_step"] = decoder_step(8, 1024, 1024, 16, steps=5)
 
     for tag, (n, k, m) in {"config4_gemm_4096": (4096, 4096, 4096),
                            "config4_gemm_16384x1024x3072": (16384, 1024, 3072)}.items():

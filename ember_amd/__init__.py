@@ -16,9 +16,9 @@ _TENSOR_NAMES = (
     "tanh", "ctgh", "T", "sum", "softmax", "sqrt", "attention", "attention_forward",
     "attention_backward", "synchronize",
 )
-_SUBMODULES = ("nn", "optim", "random", "capi", "build")
+_SUBMODULES = ("nn", "optim", "loss", "random", "capi", "build")
 
-__all__ = list(_TENSOR_NAMES) + ["nn", "optim", "random"]
+__all__ = list(_TENSOR_NAMES) + ["nn", "optim", "loss", "random"]
 
 
 def __getattr__(name: str):

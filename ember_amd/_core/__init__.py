@@ -11,15 +11,22 @@ from ._tensor import (
     _adam_step,
     _add_tensor,
     _attention_bwd,
+    _attention_bwd_packed,
     _attention_fwd,
+    _attention_fwd_packed,
+    _col_sum,
     _cos,
     _cosh,
     _ctg,
     _ctgh,
     _exponent,
     _from_numpy,
+    _gelu_bwd,
     _gt_scalar,
     _gt_tensor,
+    _layernorm_bwd,
+    _layernorm_fwd,
+    _linear,
     _log,
     _lt_scalar,
     _lt_tensor,
@@ -69,4 +76,8 @@ REFERENCE_NAMES = (
     "_Tensor", "_transpose", "_truediv_broadcasted", "_truediv_scalar", "_truediv_tensor",
 )
 
-__all__ = list(REFERENCE_NAMES) + ["_attention_fwd", "_attention_bwd", "_adam_step", "_synchronize"]
+__all__ = list(REFERENCE_NAMES) + [
+    "_attention_fwd", "_attention_bwd", "_attention_fwd_packed", "_attention_bwd_packed",
+    "_adam_step", "_linear", "_gelu_bwd", "_col_sum", "_layernorm_fwd", "_layernorm_bwd",
+    "_synchronize",
+]

@@ -38,6 +38,8 @@ HIP_SOURCES = [
     ("attention_bwd.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]),
     ("attention_bwd_c128.hip", []),
     ("optim.hip", []),
+    ("layernorm.hip", []),
+    ("block_ops.hip", []),
 ]
 
 HIP_FLAGS = [

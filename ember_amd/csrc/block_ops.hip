@@ -1,0 +1,93 @@
+// block_ops.hip -- the element-wise and reduction pieces a transformer block's
+// backward needs beside the GEMMs and attention: Ember's GELU backward and
+// the column sums that give bias gradients.
+//
+//   gelu_bwd: dx = dy * ((1 + tanh(0.8u)) * (0.5 + 0.8(u - y)))
+//             (ember/nn/activations.py:61-66, evaluated in the order of
+//             Ember's element-wise operators; u = GELU input, y = output)
+//   col_sum:  out[c] = sum_r x[r][c], the bias gradient of a Linear layer
+//             (ember/nn/layers.py:53, em.sum(grad_y, axis=0)); two launches,
+//             per-slice partial sums then their sum in slice order, so the
+//             result is deterministic.
+// Both HBM-bound.
+#include <math.h>
+
+#include "common.h"
+
+namespace ember {
+namespace {
+
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(const float *__restrict__ dy,
+                                                       const float *__restrict__ u,
+                                                       const float *__restrict__ y,
+                                                       float *__restrict__ dx, int64_t n)
+{
+#pragma clang fp contract(off)
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float x = u[i];
+        const float t = tanhf(x * 0.8f) + 1.0f;
+        const float r = (x - y[i]) * 0.8f + 0.5f;
+        dx[i] = dy[i] * (t * r);
+    }
+}
+
+constexpr int kRowsPerSlice = 128;
+
+__global__ __launch_bounds__(256) void col_sum_partial(const float *__restrict__ x,
+                                                       float *__restrict__ part, int64_t rows,
+                                                       int cols)
+{
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    const int64_t r0 = (int64_t)blockIdx.y * kRowsPerSlice;
+    const int64_t r1 = r0 + kRowsPerSlice < rows ? r0 + kRowsPerSlice : rows;
+    float s = 0.0f;
+    for (int64_t r = r0; r < r1; ++r) s += x[r * cols + c];
+    part[(int64_t)blockIdx.y * cols + c] = s;
+}
+
+__global__ __launch_bounds__(256) void col_sum_final(const float *__restrict__ part,
+                                                     float *__restrict__ out, int slices, int cols)
+{
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.0f;
+    for (int k = 0; k < slices; ++k) s += part[(int64_t)k * cols + c];
+    out[c] = s;
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" int gelu_bwd(const float *dy, const float *u, const float *y, float *dx, int64_t n)
+{
+    using namespace ember;
+    if (n < 0) return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd");
+    if (n == 0) return EMBER_OK;
+    if (!dy || !u || !y || !dx) return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd");
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(gelu_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, 0, dy, u, y, dx, n);
+    return launch_ok("gelu_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
+extern "C" int col_sum(const float *x, float *out, int64_t rows, int64_t cols)
+{
+    using namespace ember;
+    if (rows < 0 || cols < 0 || cols > INT32_MAX) return record_error(EMBER_ERR_INVALID_ARGUMENT, "col_sum");
+    if (cols == 0) return EMBER_OK;
+    if (!out || (rows > 0 && !x)) return record_error(EMBER_ERR_INVALID_ARGUMENT, "col_sum");
+    const int64_t slices = (rows + kRowsPerSlice - 1) / kRowsPerSlice;
+    if (slices > 65535) return record_error(EMBER_ERR_UNSUPPORTED, "col_sum");
+    float *part = nullptr;
+    if (slices > 0) {
+        part = (float *)scratch(kScratchColSum, (size_t)slices * cols * sizeof(float));
+        if (!part) return EMBER_ERR_OUT_OF_MEMORY;
+        hipLaunchKernelGGL(col_sum_partial, dim3((unsigned)((cols + 255) / 256), (unsigned)slices),
+                           dim3(256), 0, 0, x, part, rows, (int)cols);
+        if (!launch_ok("col_sum_partial")) return EMBER_ERR_DEVICE;
+    }
+    hipLaunchKernelGGL(col_sum_final, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, 0,
+                       (const float *)part, out, (int)slices, (int)cols);
+    return launch_ok("col_sum_final") ? EMBER_OK : EMBER_ERR_DEVICE;
+}

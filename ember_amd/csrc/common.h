@@ -26,6 +26,12 @@ bool launch_ok(const char *kernel);
 // the life of the process.  Slot ids keep independent users apart.
 void *scratch(int slot, size_t bytes);
 
-enum ScratchSlot { kScratchAttnDelta = 0, kScratchSum = 1, kScratchSlots = 4 };
+enum ScratchSlot {
+    kScratchAttnDelta = 0,
+    kScratchSum = 1,
+    kScratchLayerNorm = 2,
+    kScratchColSum = 3,
+    kScratchSlots = 4
+};
 
 }  // namespace ember

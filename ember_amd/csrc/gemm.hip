@@ -36,7 +36,31 @@ struct GemmArgs {
     int n, m, k;
     int64_t sa, sb, sc;  // batch strides (elements)
     int tiles_n, tiles_m;
+    // Epilogue (all optional): out = act(acc + bias[col]) + residual, with
+    // pre = acc + bias stored before the activation; residual and pre use
+    // out's layout and batch stride.
+    const float *bias;
+    const float *residual;
+    float *pre;
+    int act;  // 0 none, 1 Ember's GELU
 };
+
+// Ember's GELU, 0.5*x*(1 + tanh(0.8*x)) (ember/nn/activations.py:58), in the
+// order Ember's element-wise operators evaluate it.
+__device__ __forceinline__ float gelu08(float x)
+{
+#pragma clang fp contract(off)
+    return (x * 0.5f) * (tanhf(x * 0.8f) + 1.0f);
+}
+
+__device__ __forceinline__ float epilogue(const GemmArgs &g, float v, int64_t off, int col)
+{
+    if (g.bias) v += g.bias[col];
+    if (g.pre) g.pre[off] = v;
+    if (g.act == 1) v = gelu08(v);
+    if (g.residual) v += g.residual[off];
+    return v;
+}
 
 __device__ __forceinline__ int bs_index(int kr, int col)
 {
@@ -178,7 +202,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(GemmArgs g)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = row0 + 64 * wr + 32 * rb2 + acc_row(i, h32);
-                if (row < g.n) C[(int64_t)row * g.m + col] = acc[rb2][cb][i];
+                if (row < g.n) {
+                    const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)row * g.m + col;
+                    C[(int64_t)row * g.m + col] = epilogue(g, acc[rb2][cb][i], off, col);
+                }
             }
         }
     }
@@ -311,19 +338,23 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
             f32x4 v;
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) v[cb] = acc[rb][cb][i];
+            if (g.bias || g.pre || g.act || g.residual) {
+                const int col = col0 + 128 * wc + 4 * l32;
+                const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)(row0 + row) * g.m + col;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) v[cb] = epilogue(g, v[cb], off + cb, col + cb);
+            }
             *(f32x4 *)&C[(int64_t)row * g.m + 128 * wc + 4 * l32] = v;
         }
     }
 }
 
-void gemm_launch(const float *a, const float *b, float *out, int batch, int n, int m, int k,
-                 const char *who)
+int gemm_launch(const float *a, const float *b, float *out, int batch, int n, int m, int k,
+                const char *who, const float *bias = nullptr, const float *residual = nullptr,
+                float *pre = nullptr, int act = 0)
 {
-    if (n < 0 || m < 0 || k < 0 || batch < 0) {
-        record_error(EMBER_ERR_INVALID_ARGUMENT, who);
-        return;
-    }
-    if ((int64_t)n * m == 0 || batch == 0) return;
+    if (n < 0 || m < 0 || k < 0 || batch < 0) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    if ((int64_t)n * m == 0 || batch == 0) return EMBER_OK;
     GemmArgs g;
     g.a = a;
     g.b = b;
@@ -336,25 +367,25 @@ void gemm_launch(const float *a, const float *b, float *out, int batch, int n, i
     g.sc = (int64_t)n * m;
     g.tiles_n = (n + BM - 1) / BM;
     g.tiles_m = (m + BN - 1) / BN;
-    if (batch > 65535) {
-        record_error(EMBER_ERR_UNSUPPORTED, who);
-        return;
-    }
+    g.bias = bias;
+    g.residual = residual;
+    g.pre = pre;
+    g.act = act;
+    if (batch > 65535) return record_error(EMBER_ERR_UNSUPPORTED, who);
     const bool vec = (k % 4 == 0) && (m % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
     if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 && ((uintptr_t)out % 16) == 0) {
         g.tiles_n = n / FM;
         g.tiles_m = m / FN;
         hipLaunchKernelGGL(gemm_f32_dma_kernel, dim3(g.tiles_n * g.tiles_m, batch), dim3(kThreads),
                            0, 0, g);
-        launch_ok(who);
-        return;
+        return launch_ok(who) ? EMBER_OK : EMBER_ERR_DEVICE;
     }
     const dim3 grid(g.tiles_n * g.tiles_m, batch);
     if (vec)
         hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(kThreads), 0, 0, g);
     else
         hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(kThreads), 0, 0, g);
-    launch_ok(who);
+    return launch_ok(who) ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 }  // namespace
@@ -370,6 +401,13 @@ void matmul(const float *a, const float *b, float *out, int n, int m, int k)
 void matmul_batched(const float *a, const float *b, float *out, int batch, int n, int m, int k)
 {
     ember::gemm_launch(a, b, out, batch, n, m, k, "matmul_batched");
+}
+
+int linear_fwd(const float *a, const float *b, const float *bias, const float *residual,
+               float *out, float *pre, int n, int m, int k, int act)
+{
+    if (act < 0 || act > 1) return ember::record_error(EMBER_ERR_INVALID_ARGUMENT, "linear_fwd");
+    return ember::gemm_launch(a, b, out, 1, n, m, k, "linear_fwd", bias, residual, pre, act);
 }
 
 }  // extern "C"

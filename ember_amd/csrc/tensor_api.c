@@ -626,6 +626,212 @@ static PyObject *py_attention_bwd(PyObject *module, PyObject *args)
     return Py_BuildValue("(NNN)", (PyObject *)g[0], (PyObject *)g[1], (PyObject *)g[2]);
 }
 
+/* ---- transformer-block pieces (config 5) ---- */
+
+static TensorObject *opt_tensor(PyObject *o, const char *name)
+{
+    if (o == Py_None) return NULL;
+    if (!PyObject_TypeCheck(o, &TensorType)) {
+        PyErr_Format(PyExc_TypeError, "%s must be a _Tensor or None", name);
+        return (TensorObject *)-1;
+    }
+    return (TensorObject *)o;
+}
+
+/* _linear(x, w, bias|None, residual|None, n, m, k, act, want_pre) -> (y, pre|None):
+ * y = act(x @ w + bias) + residual, one GEMM with a fused epilogue. */
+static PyObject *py_linear(PyObject *module, PyObject *args)
+{
+    TensorObject *x, *w;
+    PyObject *bo, *ro;
+    int n, m, k, act, want_pre;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!OOiiiip", &TensorType, &x, &TensorType, &w, &bo, &ro, &n, &m,
+                          &k, &act, &want_pre))
+        return NULL;
+    TensorObject *bias = opt_tensor(bo, "bias"), *res = opt_tensor(ro, "residual");
+    if (bias == (TensorObject *)-1 || res == (TensorObject *)-1) return NULL;
+    if (n < 0 || m < 0 || k < 0 || x->size != (Py_ssize_t)n * k || w->size != (Py_ssize_t)k * m ||
+        (bias && bias->size != m) || (res && res->size != (Py_ssize_t)n * m)) {
+        PyErr_SetString(PyExc_ValueError, "_linear: operand sizes do not match (n, m, k)");
+        return NULL;
+    }
+    TensorObject *y = alloc_tensor((Py_ssize_t)n * m);
+    if (!y) return NULL;
+    TensorObject *pre = NULL;
+    if (want_pre && !(pre = alloc_tensor((Py_ssize_t)n * m))) {
+        Py_DECREF(y);
+        return NULL;
+    }
+    int st = linear_fwd(x->d_ptr, w->d_ptr, bias ? bias->d_ptr : NULL, res ? res->d_ptr : NULL,
+                        y->d_ptr, pre ? pre->d_ptr : NULL, n, m, k, act);
+    if (raise_status(st, "_linear")) {
+        Py_DECREF(y);
+        Py_XDECREF(pre);
+        return NULL;
+    }
+    if (!pre) return Py_BuildValue("(NO)", (PyObject *)y, Py_None);
+    return Py_BuildValue("(NN)", (PyObject *)y, (PyObject *)pre);
+}
+
+static PyObject *py_gelu_bwd(PyObject *module, PyObject *args)
+{
+    TensorObject *dy, *u, *y;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!O!", &TensorType, &dy, &TensorType, &u, &TensorType, &y)) return NULL;
+    if (dy->size != u->size || y->size != u->size) {
+        PyErr_SetString(PyExc_ValueError, "_gelu_bwd: size mismatch");
+        return NULL;
+    }
+    TensorObject *dx = alloc_tensor(u->size);
+    if (!dx) return NULL;
+    int st = gelu_bwd(dy->d_ptr, u->d_ptr, y->d_ptr, dx->d_ptr, u->size);
+    if (raise_status(st, "_gelu_bwd")) {
+        Py_DECREF(dx);
+        return NULL;
+    }
+    return (PyObject *)dx;
+}
+
+static PyObject *py_col_sum(PyObject *module, PyObject *args)
+{
+    TensorObject *x;
+    long long rows, cols;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!LL", &TensorType, &x, &rows, &cols)) return NULL;
+    if (rows < 0 || cols < 0 || x->size != (Py_ssize_t)(rows * cols)) {
+        PyErr_SetString(PyExc_ValueError, "_col_sum: size mismatch");
+        return NULL;
+    }
+    TensorObject *out = alloc_tensor((Py_ssize_t)cols);
+    if (!out) return NULL;
+    int st = col_sum(x->d_ptr, out->d_ptr, rows, cols);
+    if (raise_status(st, "_col_sum")) {
+        Py_DECREF(out);
+        return NULL;
+    }
+    return (PyObject *)out;
+}
+
+static PyObject *py_layernorm_fwd(PyObject *module, PyObject *args)
+{
+    TensorObject *x, *g, *b;
+    long long rows, d;
+    float eps;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!O!LLf", &TensorType, &x, &TensorType, &g, &TensorType, &b, &rows,
+                          &d, &eps))
+        return NULL;
+    if (rows < 0 || d <= 0 || x->size != (Py_ssize_t)(rows * d) || g->size != d || b->size != d) {
+        PyErr_SetString(PyExc_ValueError, "_layernorm_fwd: size mismatch");
+        return NULL;
+    }
+    TensorObject *y = alloc_tensor(x->size), *mean = NULL, *rstd = NULL;
+    if (!y || !(mean = alloc_tensor((Py_ssize_t)rows)) || !(rstd = alloc_tensor((Py_ssize_t)rows))) {
+        Py_XDECREF(y);
+        Py_XDECREF(mean);
+        return NULL;
+    }
+    int st = layernorm_fwd(x->d_ptr, g->d_ptr, b->d_ptr, y->d_ptr, mean->d_ptr, rstd->d_ptr, rows, d, eps);
+    if (raise_status(st, "_layernorm_fwd")) {
+        Py_DECREF(y);
+        Py_DECREF(mean);
+        Py_DECREF(rstd);
+        return NULL;
+    }
+    return Py_BuildValue("(NNN)", (PyObject *)y, (PyObject *)mean, (PyObject *)rstd);
+}
+
+static PyObject *py_layernorm_bwd(PyObject *module, PyObject *args)
+{
+    TensorObject *x, *g, *mean, *rstd, *dy;
+    long long rows, d;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!O!O!O!LL", &TensorType, &x, &TensorType, &g, &TensorType, &mean,
+                          &TensorType, &rstd, &TensorType, &dy, &rows, &d))
+        return NULL;
+    if (rows < 0 || d <= 0 || x->size != (Py_ssize_t)(rows * d) || dy->size != x->size ||
+        g->size != d || mean->size != rows || rstd->size != rows) {
+        PyErr_SetString(PyExc_ValueError, "_layernorm_bwd: size mismatch");
+        return NULL;
+    }
+    TensorObject *dx = alloc_tensor(x->size), *dg = NULL, *db = NULL;
+    if (!dx || !(dg = alloc_tensor((Py_ssize_t)d)) || !(db = alloc_tensor((Py_ssize_t)d))) {
+        Py_XDECREF(dx);
+        Py_XDECREF(dg);
+        return NULL;
+    }
+    int st = layernorm_bwd(x->d_ptr, g->d_ptr, mean->d_ptr, rstd->d_ptr, dy->d_ptr, dx->d_ptr,
+                           dg->d_ptr, db->d_ptr, rows, d);
+    if (raise_status(st, "_layernorm_bwd")) {
+        Py_DECREF(dx);
+        Py_DECREF(dg);
+        Py_DECREF(db);
+        return NULL;
+    }
+    return Py_BuildValue("(NNN)", (PyObject *)dx, (PyObject *)dg, (PyObject *)db);
+}
+
+/* Packed projections: qkv is (B, S, 3, H, D) (a QKV Linear's output), o is
+ * (B, S, H, D); attention reads and writes them through strides, no copies. */
+static PyObject *py_attention_fwd_packed(PyObject *module, PyObject *args)
+{
+    TensorObject *qkv;
+    long long B, S, H, D;
+    float scale;
+    int causal;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!LLLLfp", &TensorType, &qkv, &B, &S, &H, &D, &scale, &causal))
+        return NULL;
+    if (B < 0 || S < 0 || H < 0 || D <= 0 || qkv->size != (Py_ssize_t)(B * S * 3 * H * D)) {
+        PyErr_SetString(PyExc_ValueError, "_attention_fwd_packed: qkv must hold B*S*3*H*D elements");
+        return NULL;
+    }
+    TensorObject *o = alloc_tensor((Py_ssize_t)(B * S * H * D)), *lse = NULL;
+    if (!o || !(lse = alloc_tensor((Py_ssize_t)(B * H * S)))) {
+        Py_XDECREF(o);
+        return NULL;
+    }
+    const int64_t hd = H * D;
+    int st = attention_fwd(qkv->d_ptr, qkv->d_ptr + hd, qkv->d_ptr + 2 * hd, o->d_ptr, lse->d_ptr, B,
+                           H, S, D, scale, causal, S * 3 * hd, D, 3 * hd, S * hd, D, hd);
+    if (raise_status(st, "_attention_fwd_packed")) {
+        Py_DECREF(o);
+        Py_DECREF(lse);
+        return NULL;
+    }
+    return Py_BuildValue("(NN)", (PyObject *)o, (PyObject *)lse);
+}
+
+static PyObject *py_attention_bwd_packed(PyObject *module, PyObject *args)
+{
+    TensorObject *qkv, *o, *lse, *d_o;
+    long long B, S, H, D;
+    float scale;
+    int causal;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!O!O!LLLLfp", &TensorType, &qkv, &TensorType, &o, &TensorType, &lse,
+                          &TensorType, &d_o, &B, &S, &H, &D, &scale, &causal))
+        return NULL;
+    if (B < 0 || S < 0 || H < 0 || D <= 0 || qkv->size != (Py_ssize_t)(B * S * 3 * H * D) ||
+        o->size != (Py_ssize_t)(B * S * H * D) || d_o->size != o->size ||
+        lse->size != (Py_ssize_t)(B * H * S)) {
+        PyErr_SetString(PyExc_ValueError, "_attention_bwd_packed: size mismatch");
+        return NULL;
+    }
+    TensorObject *g = alloc_tensor(qkv->size);
+    if (!g) return NULL;
+    const int64_t hd = H * D;
+    int st = attention_bwd(qkv->d_ptr, qkv->d_ptr + hd, qkv->d_ptr + 2 * hd, o->d_ptr, lse->d_ptr,
+                           d_o->d_ptr, g->d_ptr, g->d_ptr + hd, g->d_ptr + 2 * hd, B, H, S, D, scale,
+                           causal, S * 3 * hd, D, 3 * hd, S * hd, D, hd);
+    if (raise_status(st, "_attention_bwd_packed")) {
+        Py_DECREF(g);
+        return NULL;
+    }
+    return (PyObject *)g;
+}
+
 /* _adam_step(params, grads, means, variances, lr, beta1, beta2, eps, t):
  * lists of _Tensor of matching sizes; updates params, means, variances in
  * place with one fused launch per 48 tensors (replaces Adam.apply's 13
@@ -712,6 +918,13 @@ static PyMethodDef module_methods[] = {
     METHOD("_attention_fwd", py_attention_fwd, "fused attention forward -> (o, lse)"),
     METHOD("_attention_bwd", py_attention_bwd, "fused attention backward -> (dq, dk, dv)"),
     METHOD("_adam_step", py_adam_step, "fused Adam step over lists of _Tensor, in place"),
+    METHOD("_linear", py_linear, "act(x @ w + bias) + residual -> (y, pre)"),
+    METHOD("_gelu_bwd", py_gelu_bwd, "backward of Ember's GELU"),
+    METHOD("_col_sum", py_col_sum, "column sums (bias gradient)"),
+    METHOD("_layernorm_fwd", py_layernorm_fwd, "LayerNorm -> (y, mean, rstd)"),
+    METHOD("_layernorm_bwd", py_layernorm_bwd, "LayerNorm backward -> (dx, dgamma, dbeta)"),
+    METHOD("_attention_fwd_packed", py_attention_fwd_packed, "attention on packed (B,S,3,H,D) qkv"),
+    METHOD("_attention_bwd_packed", py_attention_bwd_packed, "backward -> packed dqkv"),
     {"_synchronize", (PyCFunction)py_synchronize, METH_NOARGS, "wait for all queued device work"},
     {NULL, NULL, 0, NULL}};
 

@@ -14,10 +14,13 @@ logsumexp instead of storing it.
 
 from __future__ import annotations
 
+import math
 from abc import ABC, abstractmethod
 from itertools import chain
 
-from ember_amd.tensor import Tensor, attention_backward, attention_forward
+from ember_amd import _core as C
+from ember_amd import random as _random
+from ember_amd.tensor import T, Tensor, attention_backward, attention_forward
 
 
 class Layer(ABC):
@@ -105,3 +108,219 @@ class Attention(Layer):
             raise RuntimeError("forward() must run before backward()")
         q, k, v = self.x
         return attention_backward(q, k, v, self.y, self.lse, grad_y, self.causal, self.scale)
+
+
+def _rows(x: Tensor) -> tuple[int, int]:
+    if len(x.shape) != 2:
+        raise ValueError(f"expected a 2-D (rows, features) Tensor, got {x.shape}")
+    return x.shape
+
+
+def linear(x: Tensor, w: Tensor, b: Tensor | None = None, residual: Tensor | None = None,
+           gelu: bool = False) -> tuple[Tensor, Tensor | None]:
+    """``act(x @ w + b) + residual`` in one GEMM with a fused epilogue; returns
+    (y, pre) where pre = x @ w + b is kept only when ``gelu`` (its backward
+    needs it)."""
+    n, k = _rows(x)
+    k2, m = _rows(w)
+    if k != k2:
+        raise ValueError(f"Shape mismatch: {x.shape} cannot multiply {w.shape}")
+    y, pre = C._linear(x._core, w._core, None if b is None else b._core,
+                       None if residual is None else residual._core, n, m, k, 1 if gelu else 0, gelu)
+    return Tensor._from_core(y, (n, m)), (Tensor._from_core(pre, (n, m)) if pre is not None else None)
+
+
+def col_sum(x: Tensor) -> Tensor:
+    """Column sums of a 2-D Tensor (a Linear layer's bias gradient)."""
+    n, m = _rows(x)
+    return Tensor._from_core(C._col_sum(x._core, n, m), (m,))
+
+
+class Linear(Layer):
+    """y = b + x @ w (``ember/nn/layers.py:9-56``), x of shape (rows, in).
+    ``activation="gelu"`` fuses Ember's GELU into the GEMM epilogue.  Weights
+    start U(+-1/sqrt(in)), biases 0, as the reference's ``reset``."""
+
+    def __init__(self, in_features: int, out_features: int, activation: str | None = None):
+        if activation not in (None, "gelu"):
+            raise ValueError(f"unsupported activation {activation!r}")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.activation = activation
+        self.reset()
+
+    def reset(self) -> None:
+        self.x = self.y = self.pre = None
+        scale = 1.0 / math.sqrt(self.in_features)
+        self.w = _random.uniform(-scale, scale, (self.in_features, self.out_features))
+        self.b = _random.zeros((self.out_features,))
+        self.grad_w = self.grad_b = None
+
+    def parameters(self) -> list[Tensor]:
+        return [self.w, self.b]
+
+    def gradients(self) -> list[Tensor | None]:
+        return [self.grad_w, self.grad_b]
+
+    def forward(self, x: Tensor, training: bool = True, residual: Tensor | None = None) -> Tensor:
+        self.x = x
+        y, self.pre = linear(x, self.w, self.b, residual, self.activation == "gelu")
+        return y
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        if self.x is None:
+            raise RuntimeError("forward() must run before backward()")
+        if self.activation == "gelu":
+            grad_y = Tensor._from_core(C._gelu_bwd(grad_y._core, self.pre._core, self.y._core),
+                                       grad_y.shape)
+        self.grad_w = T(self.x) @ grad_y
+        self.grad_b = col_sum(grad_y)
+        return grad_y @ T(self.w)
+
+
+class GELU(Layer):
+    """Ember's GELU, 0.5*x*(1 + tanh(0.8x)) (``ember/nn/activations.py:51-66``):
+    the forward composed from element-wise operators as the reference does,
+    the backward one fused kernel."""
+
+    def reset(self) -> None:
+        self.x = self.y = None
+
+    def parameters(self) -> list[Tensor]:
+        return []
+
+    def gradients(self) -> list[Tensor | None]:
+        return []
+
+    def forward(self, x: Tensor, training: bool = True) -> Tensor:
+        from ember_amd.tensor import tanh
+        return 0.5 * x * (1 + tanh(0.8 * x))
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        if self.x is None or self.y is None:
+            raise RuntimeError("forward() must run before backward()")
+        return Tensor._from_core(C._gelu_bwd(grad_y._core, self.x._core, self.y._core), grad_y.shape)
+
+
+class LayerNorm(Layer):
+    """LayerNorm over the last dimension: (x - mean)/sqrt(var + eps)*gamma + beta
+    (biased variance); gamma = 1, beta = 0 at reset."""
+
+    def __init__(self, features: int, eps: float = 1e-5):
+        self.features = features
+        self.eps = eps
+        self.reset()
+
+    def reset(self) -> None:
+        self.x = self.y = None
+        self.gamma = _random.ones((self.features,))
+        self.beta = _random.zeros((self.features,))
+        self.grad_gamma = self.grad_beta = None
+        self._stats = None
+
+    def parameters(self) -> list[Tensor]:
+        return [self.gamma, self.beta]
+
+    def gradients(self) -> list[Tensor | None]:
+        return [self.grad_gamma, self.grad_beta]
+
+    def forward(self, x: Tensor, training: bool = True) -> Tensor:
+        d = x.shape[-1]
+        rows = x.size // d
+        y, mean, rstd = C._layernorm_fwd(x._core, self.gamma._core, self.beta._core, rows, d, self.eps)
+        self._stats = (mean, rstd)
+        return Tensor._from_core(y, x.shape)
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        if self.x is None or self._stats is None:
+            raise RuntimeError("forward() must run before backward()")
+        d = self.x.shape[-1]
+        dx, dg, db = C._layernorm_bwd(self.x._core, self.gamma._core, *self._stats, grad_y._core,
+                                      self.x.size // d, d)
+        self.grad_gamma = Tensor._from_core(dg, (d,))
+        self.grad_beta = Tensor._from_core(db, (d,))
+        return Tensor._from_core(dx, self.x.shape)
+
+
+def _xavier(fan_in: int, fan_out: int) -> Tensor:
+    a = math.sqrt(6.0 / (fan_in + fan_out))
+    return _random.uniform(-a, a, (fan_in, fan_out))
+
+
+class DecoderBlock(Layer):
+    """One pre-LN transformer decoder block on (B*S, d) token rows:
+        h = LN1(x);  x2 = x + Attention(h Wqkv + bqkv) Wo + bo
+        y = x2 + GELU(LN2(x2) W1 + b1) W2 + b2
+    with causal fused attention reading the packed QKV projection in place.
+    Weights Xavier-uniform, biases 0, LayerNorm gamma 1 / beta 0.  ``forward``
+    takes (x, B, S); ``backward`` returns dx and fills ``gradients()``."""
+
+    def __init__(self, d_model: int, n_heads: int, mlp_ratio: int = 4, causal: bool = True):
+        if d_model % n_heads:
+            raise ValueError("d_model must be a multiple of n_heads")
+        self.d, self.h, self.r, self.causal = d_model, n_heads, mlp_ratio, causal
+        self.reset()
+
+    def reset(self) -> None:
+        d, r = self.d, self.r
+        self.ln1 = LayerNorm(d)
+        self.ln2 = LayerNorm(d)
+        self.w_qkv, self.b_qkv = _xavier(d, 3 * d), _random.zeros((3 * d,))
+        self.w_o, self.b_o = _xavier(d, d), _random.zeros((d,))
+        self.w_1, self.b_1 = _xavier(d, r * d), _random.zeros((r * d,))
+        self.w_2, self.b_2 = _xavier(r * d, d), _random.zeros((d,))
+        self._grads: list[Tensor | None] = [None] * 12
+        self.x = self.y = None
+        self._saved = None
+
+    def parameters(self) -> list[Tensor]:
+        return [self.ln1.gamma, self.ln1.beta, self.w_qkv, self.b_qkv, self.w_o, self.b_o,
+                self.ln2.gamma, self.ln2.beta, self.w_1, self.b_1, self.w_2, self.b_2]
+
+    def gradients(self) -> list[Tensor | None]:
+        return list(self._grads)
+
+    def __call__(self, x: Tensor, B: int, S: int, training: bool = True) -> Tensor:
+        self.x = x
+        self.y = self.forward((x, B, S), training)
+        return self.y
+
+    def forward(self, xbs, training: bool = True) -> Tensor:
+        x, B, S = xbs
+        D = self.d // self.h
+        scale = float(1.0 / math.sqrt(D))
+        self.ln1.x = x
+        h1 = self.ln1.forward(x)
+        qkv, _ = linear(h1, self.w_qkv, self.b_qkv)
+        o_core, lse = C._attention_fwd_packed(qkv._core, B, S, self.h, D, scale, self.causal)
+        o = Tensor._from_core(o_core, (B * S, self.d))
+        x2, _ = linear(o, self.w_o, self.b_o, residual=x)
+        self.ln2.x = x2
+        h2 = self.ln2.forward(x2)
+        a, u = linear(h2, self.w_1, self.b_1, gelu=True)
+        y, _ = linear(a, self.w_2, self.b_2, residual=x2)
+        self._saved = (B, S, scale, h1, qkv, o, lse, x2, h2, a, u)
+        return y
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        if self._saved is None:
+            raise RuntimeError("forward() must run before backward()")
+        B, S, scale, h1, qkv, o, lse, x2, h2, a, u = self._saved
+        D = self.d // self.h
+        # MLP: y = x2 + GELU(h2 W1 + b1) W2 + b2
+        g_w2, g_b2 = T(a) @ grad_y, col_sum(grad_y)
+        da = grad_y @ T(self.w_2)
+        du = Tensor._from_core(C._gelu_bwd(da._core, u._core, a._core), da.shape)
+        g_w1, g_b1 = T(h2) @ du, col_sum(du)
+        dx2 = self.ln2.backward(du @ T(self.w_1)) + grad_y
+        # attention: x2 = x + O Wo + bo
+        g_wo, g_bo = T(o) @ dx2, col_sum(dx2)
+        d_o = dx2 @ T(self.w_o)
+        dqkv = Tensor._from_core(
+            C._attention_bwd_packed(qkv._core, o._core, lse, d_o._core, B, S, self.h, D, scale,
+                                    self.causal), qkv.shape)
+        g_wqkv, g_bqkv = T(h1) @ dqkv, col_sum(dqkv)
+        dx = self.ln1.backward(dqkv @ T(self.w_qkv)) + dx2
+        self._grads = [self.ln1.grad_gamma, self.ln1.grad_beta, g_wqkv, g_bqkv, g_wo, g_bo,
+                       self.ln2.grad_gamma, self.ln2.grad_beta, g_w1, g_b1, g_w2, g_b2]
+        return dx

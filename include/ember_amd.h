@@ -134,6 +134,42 @@ int adam_step(float *const *params, const float *const *grads, float *const *exp
               float *const *exp_avg_sq, const int64_t *sizes, int ntensors, double lr,
               double beta1, double beta2, double eps, int64_t step);
 
+/* ---- transformer-block pieces (config 5's pre-LN decoder block) ----
+ * None has a counterpart in the reference; each replaces a composition of
+ * its element-wise operators.  All return a status and launch nothing on an
+ * argument error.  Row-major fp32, device pointers, 16-byte alignment where
+ * noted. */
+
+/* out(n x m) = act(a @ b + bias) + residual, with pre = a @ b + bias stored
+ * before the activation when pre is not NULL (what the activation's backward
+ * needs).  bias (m), residual (n x m) and pre may each be NULL; act 0 = none,
+ * 1 = Ember's GELU 0.5*x*(1 + tanh(0.8x)) (ember/nn/activations.py:58).
+ * Replaces Linear.forward's `b + x @ w` (ember/nn/layers.py:45-48) plus the
+ * activation and the residual add as separate operators. */
+int linear_fwd(const float *a, const float *b, const float *bias, const float *residual,
+               float *out, float *pre, int n, int m, int k, int act);
+
+/* dx = dy * ((1 + tanh(0.8u)) * (0.5 + 0.8(u - y))): the backward of Ember's
+ * GELU (ember/nn/activations.py:61-66) with u its input and y its output. */
+int gelu_bwd(const float *dy, const float *u, const float *y, float *dx, int64_t n);
+
+/* out[c] = sum over rows of x[r][c] (x is rows x cols): a Linear layer's bias
+ * gradient, em.sum(grad_y, axis=0) in ember/nn/layers.py:53.  Deterministic
+ * (fixed summation order); uses library scratch. */
+int col_sum(const float *x, float *out, int64_t rows, int64_t cols);
+
+/* LayerNorm over the last dimension d (d % 4 == 0, d <= 4096; all pointers
+ * 16-byte aligned and non-NULL):
+ *   mean = sum(x)/d, var = sum((x-mean)^2)/d, rstd = 1/sqrt(var + eps),
+ *   y = (x - mean)*rstd*gamma + beta;  mean and rstd (rows) are kept for
+ * the backward, which gives dx and the parameter gradients
+ *   dgamma = sum_rows(dy*xhat), dbeta = sum_rows(dy)   (xhat = (x-mean)*rstd)
+ * deterministically (fixed-order reduction over library scratch). */
+int layernorm_fwd(const float *x, const float *gamma, const float *beta, float *y, float *mean,
+                  float *rstd, int64_t rows, int64_t d, float eps);
+int layernorm_bwd(const float *x, const float *gamma, const float *mean, const float *rstd,
+                  const float *dy, float *dx, float *dgamma, float *dbeta, int64_t rows, int64_t d);
+
 #undef EMBER_BINARY_OP
 #undef EMBER_SCALAR_OP
 #undef EMBER_BROADCAST_OP

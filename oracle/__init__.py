@@ -62,6 +62,10 @@ def lib() -> C.CDLL:
         L.oracle_attention_bwd.argtypes = [_f32p] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
         L.oracle_attention_bwd.restype = C.c_int
         L.oracle_adam_step.argtypes = [_f32p] * 4 + [_i64] + [C.c_double] * 4 + [_i64]
+        L.oracle_layernorm_fwd.argtypes = [_f32p] * 6 + [_i64, _i64, C.c_float]
+        L.oracle_layernorm_bwd.argtypes = [_f32p] * 8 + [_i64, _i64]
+        L.oracle_gelu_fwd.argtypes = [_f32p, _f32p, _i64]
+        L.oracle_gelu_bwd.argtypes = [_f32p] * 4 + [_i64]
         _lib = L
     return _lib
 
@@ -86,9 +90,9 @@ def ref_lib() -> C.CDLL:
             getattr(L, name).argtypes = [_f32p, _f32p, _f32p, C.c_int]
         for name in ("mul_scalar", "add_scalar", "truediv_scalar"):
             getattr(L, name).argtypes = [_f32p, C.c_float, _f32p, C.c_int]
-        for name in ("exponent_tensor", "sqrt_tensor"):
+        for name in ("exponent_tensor", "sqrt_tensor", "tanh_tensor"):
             getattr(L, name).argtypes = [_f32p, _f32p, C.c_int]
-        for name in ("sub_broadcasted", "truediv_broadcasted", "mul_broadcasted"):
+        for name in ("sub_broadcasted", "truediv_broadcasted", "mul_broadcasted", "add_broadcasted"):
             getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _i32p, _i32p, _i32p, C.c_int]
         _ref = L
     return _ref
@@ -295,3 +299,83 @@ def ref_composed_adam_step(p, g, m, v, lr, beta1, beta2, eps, t):
     den = scal("add_scalar", sq, eps)                                     # sqrt(v_hat) + eps
     p = ten("sub_tensor", p, ten("truediv_tensor", num, den))             # p -= num / den
     return p, m, v
+
+
+# --------------------------------------------- LayerNorm, GELU (block pieces)
+
+
+def _f32c(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def layernorm_fwd(x, gamma, beta, eps=1e-5):
+    """(y, mean, rstd) of LayerNorm over the last axis, FP64 inside."""
+    x, gamma, beta = _f32c(x), _f32c(gamma), _f32c(beta)
+    d = x.shape[-1]
+    rows = x.size // d
+    y = np.empty_like(x)
+    mean = np.empty(x.shape[:-1], np.float32)
+    rstd = np.empty(x.shape[:-1], np.float32)
+    lib().oracle_layernorm_fwd(x, gamma, beta, y, mean, rstd, rows, d, eps)
+    return y, mean, rstd
+
+
+def layernorm_bwd(x, gamma, mean, rstd, dy):
+    """(dx, dgamma, dbeta) from the forward's mean / rstd, FP64 inside."""
+    x, gamma, mean, rstd, dy = (_f32c(a) for a in (x, gamma, mean, rstd, dy))
+    d = x.shape[-1]
+    dx = np.empty_like(x)
+    dg = np.empty(d, np.float32)
+    db = np.empty(d, np.float32)
+    lib().oracle_layernorm_bwd(x, gamma, mean, rstd, dy, dx, dg, db, x.size // d, d)
+    return dx, dg, db
+
+
+def gelu_fwd(x):
+    x = _f32c(x)
+    y = np.empty_like(x)
+    lib().oracle_gelu_fwd(x, y, x.size)
+    return y
+
+
+def gelu_bwd(dy, x, y):
+    dy, x, y = _f32c(dy), _f32c(x), _f32c(y)
+    dx = np.empty_like(x)
+    lib().oracle_gelu_bwd(dy, x, y, dx, x.size)
+    return dx
+
+
+def ref_composed_gelu(x, dy):
+    """Ember's GELU forward and backward (ember/nn/activations.py:56-66) run
+    through the reference's own compiled operators, in Python's evaluation
+    order.  Returns (y, dx)."""
+    R = ref_lib()
+    x, dy = _f32c(x).reshape(-1), _f32c(dy).reshape(-1)
+    n = x.size
+    f32 = np.float32
+
+    def new():
+        return np.empty(n, np.float32)
+
+    def scal(fn, a, v):
+        out = new()
+        getattr(R, fn)(a, f32(v), out, n)
+        return out
+
+    def ten(fn, a, b):
+        out = new()
+        getattr(R, fn)(a, b, out, n)
+        return out
+
+    def tanh(a):
+        out = new()
+        R.tanh_tensor(a, out, n)
+        return out
+
+    # y = 0.5 * x * (1 + em.tanh(0.8 * x))
+    y = ten("mul_tensor", scal("mul_scalar", x, 0.5), scal("add_scalar", tanh(scal("mul_scalar", x, 0.8)), 1.0))
+    # grad_y * ((1.0 + em.tanh(a * x)) * (0.5 + a * (x - y)))
+    t = scal("add_scalar", tanh(scal("mul_scalar", x, 0.8)), 1.0)
+    r = scal("add_scalar", scal("mul_scalar", ten("sub_tensor", x, y), 0.8), 0.5)
+    dx = ten("mul_tensor", dy, ten("mul_tensor", t, r))
+    return y, dx

@@ -226,3 +226,80 @@ void oracle_adam_step(float *p, const float *g, float *m, float *v, int64_t n, d
         v[i] = vi;
     }
 }
+
+/* ---- LayerNorm (build-defined; Ember has none) ----
+ * mean, var (biased) and the backward's row means in FP64, outputs cast to
+ * float once, Ember style.  Row-major (rows x d). */
+void oracle_layernorm_fwd(const float *x, const float *gamma, const float *beta, float *y,
+                          float *mean, float *rstd, int64_t rows, int64_t d, float eps)
+{
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * d;
+        double s = 0.0;
+        for (int64_t c = 0; c < d; c++) s += xr[c];
+        const double mu = s / (double)d;
+        double q = 0.0;
+        for (int64_t c = 0; c < d; c++) q += ((double)xr[c] - mu) * ((double)xr[c] - mu);
+        const double rs = 1.0 / sqrt(q / (double)d + (double)eps);
+        for (int64_t c = 0; c < d; c++)
+            y[r * d + c] = (float)(((double)xr[c] - mu) * rs * (double)gamma[c] + (double)beta[c]);
+        mean[r] = (float)mu;
+        rstd[r] = (float)rs;
+    }
+}
+
+/* Backward from the given x and the float mean / rstd the forward stored. */
+void oracle_layernorm_bwd(const float *x, const float *gamma, const float *mean, const float *rstd,
+                          const float *dy, float *dx, float *dgamma, float *dbeta, int64_t rows,
+                          int64_t d)
+{
+    double *dg = (double *)calloc((size_t)(d > 0 ? d : 1), sizeof(double));
+    double *db = (double *)calloc((size_t)(d > 0 ? d : 1), sizeof(double));
+    for (int64_t r = 0; r < rows; r++) {
+        const double mu = mean[r], rs = rstd[r];
+        double m1 = 0.0, m2 = 0.0;
+        for (int64_t c = 0; c < d; c++) {
+            const double xh = ((double)x[r * d + c] - mu) * rs;
+            const double g = (double)dy[r * d + c] * (double)gamma[c];
+            m1 += g;
+            m2 += g * xh;
+            dg[c] += (double)dy[r * d + c] * xh;
+            db[c] += (double)dy[r * d + c];
+        }
+        m1 /= (double)d;
+        m2 /= (double)d;
+        for (int64_t c = 0; c < d; c++) {
+            const double xh = ((double)x[r * d + c] - mu) * rs;
+            const double g = (double)dy[r * d + c] * (double)gamma[c];
+            dx[r * d + c] = (float)(rs * (g - m1 - xh * m2));
+        }
+    }
+    for (int64_t c = 0; c < d; c++) {
+        dgamma[c] = (float)dg[c];
+        dbeta[c] = (float)db[c];
+    }
+    free(dg);
+    free(db);
+}
+
+/* ---- Ember's GELU (ember/nn/activations.py:56-66), operator by operator ----
+ * forward  y  = (x*0.5) * (tanh(x*0.8) + 1)
+ * backward dx = dy * ((tanh(x*0.8) + 1) * ((x - y)*0.8 + 0.5))
+ * each step one fp32 operation (built with -ffp-contract=off). */
+void oracle_gelu_fwd(const float *x, float *y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        const float a = x[i] * 0.5f;
+        const float t = tanhf(x[i] * 0.8f) + 1.0f;
+        y[i] = a * t;
+    }
+}
+
+void oracle_gelu_bwd(const float *dy, const float *x, const float *y, float *dx, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) {
+        const float t = tanhf(x[i] * 0.8f) + 1.0f;
+        const float r = (x[i] - y[i]) * 0.8f + 0.5f;
+        dx[i] = dy[i] * (t * r);
+    }
+}

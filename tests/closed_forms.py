@@ -64,3 +64,33 @@ def finite_difference_grads(q, k, v, d_o, causal: bool, scale: float, eps: float
             g[idx] = (fp - fm) / (2 * eps)
         grads.append(g)
     return tuple(grads)
+
+
+def layernorm(x, gamma, beta, eps):
+    """float64 LayerNorm over the last axis (biased variance)."""
+    x = np.asarray(x, np.float64)
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * np.asarray(gamma, np.float64) + np.asarray(beta, np.float64)
+
+
+def layernorm_grads_fd(x, gamma, beta, dy, eps, h=1e-6):
+    """Central differences of f = <LayerNorm(x), dy> w.r.t. x, gamma, beta."""
+    x, gamma, beta, dy = (np.array(a, np.float64) for a in (x, gamma, beta, dy))
+
+    def f():
+        return float((layernorm(x, gamma, beta, eps) * dy).sum())
+
+    out = []
+    for a in (x, gamma, beta):
+        g = np.zeros_like(a)
+        for idx in np.ndindex(*a.shape):
+            old = a[idx]
+            a[idx] = old + h
+            fp = f()
+            a[idx] = old - h
+            fm = f()
+            a[idx] = old
+            g[idx] = (fp - fm) / (2 * h)
+        out.append(g)
+    return tuple(out)

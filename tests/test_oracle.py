@@ -273,3 +273,134 @@ def test_oracle_adam_planted_mistakes_fail():
     bad = [x.copy() for x in base]
     oracle.adam_step(*bad, lr, b1, b2, eps, 1000)   # bias corrections ~1
     assert not np.allclose(bad[0], good[0], rtol=1e-6)
+
+
+# ------------------------------------------------------ LayerNorm and GELU
+
+
+@needs_ref
+def test_oracle_gelu_is_bitwise_the_reference_composition():
+    x, dy = _rand((3000,), 71), _rand((3000,), 72)
+    y_ref, dx_ref = oracle.ref_composed_gelu(x, dy)
+    y = oracle.gelu_fwd(x)
+    assert np.array_equal(y, y_ref)
+    assert np.array_equal(oracle.gelu_bwd(dy, x, y), dx_ref)
+
+
+def test_gelu_backward_formula_is_the_derivative():
+    """Ember's backward formula (activations.py:65-66) equals d/dx of its
+    forward, by central differences in float64."""
+    x = np.linspace(-4, 4, 81)
+    f = lambda z: 0.5 * z * (1 + np.tanh(0.8 * z))  # noqa: E731
+    h = 1e-6
+    fd = (f(x + h) - f(x - h)) / (2 * h)
+    y = f(x)
+    np.testing.assert_allclose((1 + np.tanh(0.8 * x)) * (0.5 + 0.8 * (x - y)), fd, rtol=1e-7, atol=1e-9)
+    np.testing.assert_allclose(oracle.gelu_bwd(np.ones(81), x, oracle.gelu_fwd(x)), fd, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("rows,d", [(1, 4), (7, 64), (33, 1024), (3, 4096)])
+def test_oracle_layernorm_forward_closed_form(rows, d):
+    x = _rand((rows, d), 73) * 3 + 1
+    g, b = _rand((d,), 74), _rand((d,), 75)
+    y, mean, rstd = oracle.layernorm_fwd(x, g, b, 1e-5)
+    np.testing.assert_allclose(y, closed_forms.layernorm(x, g, b, 1e-5), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(mean, x.astype(np.float64).mean(-1), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(rstd, 1 / np.sqrt(x.astype(np.float64).var(-1) + 1e-5), rtol=1e-6)
+
+
+def test_oracle_layernorm_backward_finite_differences():
+    rows, d = 3, 8
+    x, dy = _rand((rows, d), 76), _rand((rows, d), 77)
+    g, b = _rand((d,), 78), _rand((d,), 79)
+    _, mean, rstd = oracle.layernorm_fwd(x, g, b, 1e-5)
+    dx, dg, db = oracle.layernorm_bwd(x, g, mean, rstd, dy)
+    fx, fg, fb = closed_forms.layernorm_grads_fd(x, g, b, dy, 1e-5)
+    np.testing.assert_allclose(dx, fx, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(dg, fg, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(db, fb, rtol=1e-6, atol=1e-6)
+    # planted mistake: the mean(g * xhat) term dropped
+    xh = (x.astype(np.float64) - mean[:, None]) * rstd[:, None]
+    gg = dy * g
+    wrong = rstd[:, None] * (gg - gg.mean(-1, keepdims=True))
+    assert not np.allclose(wrong, fx, rtol=1e-3, atol=1e-4)
+    del xh
+
+
+@needs_ref
+def test_oracle_layernorm_matches_reference_composition():
+    """LayerNorm written with the reference's own operators (sum_axis, broadcast
+    sub / mul / div / add, sqrt), the way Ember would have to compose it."""
+    R = oracle.ref_lib()
+    rows, d = 16, 96
+    x = _rand((rows, d), 80)
+    g, b = _rand((d,), 81), _rand((d,), 82)
+    s = np.empty((rows, 1), np.float32)
+    R.sum_axis(x, s, rows, 1, d)
+    mu = s / np.float32(d)
+    shp, sa, sb = oracle._bcast((rows, d), (rows, 1))
+    xc = np.empty((rows, d), np.float32)
+    R.sub_broadcasted(x, np.ascontiguousarray(mu), xc, shp, sa, sb, 2)
+    sq = np.empty_like(xc)
+    R.mul_tensor(xc, xc, sq, rows * d)
+    v = np.empty((rows, 1), np.float32)
+    R.sum_axis(sq, v, rows, 1, d)
+    den = np.empty_like(v)
+    R.sqrt_tensor(np.ascontiguousarray(v / np.float32(d) + np.float32(1e-5)), den, rows)
+    xh = np.empty_like(xc)
+    R.truediv_broadcasted(xc, den, xh, shp, sa, sb, 2)
+    shp2, sa2, sb2 = oracle._bcast((rows, d), (1, d))
+    t = np.empty_like(xh)
+    R.mul_broadcasted(xh, np.ascontiguousarray(g.reshape(1, d)), t, shp2, sa2, sb2, 2)
+    y_ref = np.empty_like(t)
+    R.add_broadcasted(t, np.ascontiguousarray(b.reshape(1, d)), y_ref, shp2, sa2, sb2, 2)
+    y, _, _ = oracle.layernorm_fwd(x, g, b, 1e-5)
+    np.testing.assert_allclose(y, y_ref, rtol=1e-5, atol=1e-5)
+
+
+# -------------------------------------------- config 5's decoder block
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_decoder_oracle_backward_finite_differences(causal):
+    """oracle/decoder.py's backward equals central differences of
+    f = <block(x), dy> for every input and parameter (float64)."""
+    from oracle import decoder
+
+    B, S, H, d, r = 2, 3, 2, 8, 2
+    rng = np.random.default_rng(90)
+    params = decoder.init_params(d, H, r, rng)
+    x = rng.standard_normal((B * S, d))
+    dy = rng.standard_normal((B * S, d))
+    y, cache = decoder.forward(params, x, B, S, H, causal)
+    dx, grads = decoder.backward(params, cache, dy, B, S, H)
+
+    def f():
+        return float((decoder.forward(params, x, B, S, H, causal)[0] * dy).sum())
+
+    h = 1e-6
+    for arr, g in [(x, dx)] + list(zip(params, grads)):
+        fd = np.zeros_like(arr)
+        for idx in np.ndindex(*arr.shape):
+            old = arr[idx]
+            arr[idx] = old + h
+            fp = f()
+            arr[idx] = old - h
+            fm = f()
+            arr[idx] = old
+            fd[idx] = (fp - fm) / (2 * h)
+        np.testing.assert_allclose(g, fd, rtol=1e-5, atol=1e-7)
+
+
+def test_decoder_oracle_causal_rows_see_only_the_past():
+    from oracle import decoder
+
+    B, S, H, d = 1, 5, 2, 8
+    rng = np.random.default_rng(91)
+    params = decoder.init_params(d, H, 2, rng)
+    x = rng.standard_normal((S, d))
+    y, _ = decoder.forward(params, x, B, S, H, True)
+    x2 = x.copy()
+    x2[3:] += 1.0
+    y2, _ = decoder.forward(params, x2, B, S, H, True)
+    np.testing.assert_array_equal(y[:3], y2[:3])
