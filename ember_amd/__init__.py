@@ -14,7 +14,7 @@ import importlib
 _TENSOR_NAMES = (
     "Tensor", "max", "min", "amax", "exp", "log", "sin", "cos", "tan", "ctg", "sinh", "cosh",
     "tanh", "ctgh", "T", "sum", "softmax", "sqrt", "attention", "attention_forward",
-    "attention_backward", "synchronize",
+    "attention_backward", "synchronize", "empty_cache", "memory_stats",
 )
 _SUBMODULES = ("nn", "optim", "loss", "random", "capi", "build")
 

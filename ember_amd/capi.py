@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
     L.copy_to_device.argtypes = [_vp, _vp, C.c_size_t]
     L.copy_from_device.argtypes = [_vp, _vp, C.c_size_t]
     L.sync_device.argtypes = []
+    L.ember_empty_cache.argtypes = []
+    L.ember_memory_stats.argtypes = [C.POINTER(C.c_size_t)] * 3
     L.matmul.argtypes = [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]
     L.matmul_batched.argtypes = [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int]
     L.transpose.argtypes = [_vp, _vp, C.c_int, C.c_int]
@@ -73,6 +75,8 @@ def lib() -> C.CDLL:
     L.attention_fwd.argtypes = [_vp] * 5 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
     L.attention_bwd.restype = C.c_int
     L.attention_bwd.argtypes = [_vp] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
+    L.gemm_ex.restype = C.c_int
+    L.gemm_ex.argtypes = [_vp] * 3 + [C.c_int] * 6 + [_vp] * 3 + [C.c_int]
     L.adam_step.restype = C.c_int
     L.adam_step.argtypes = [C.POINTER(_vp)] * 4 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 4 + [_i64]
     _lib = L

@@ -31,7 +31,8 @@ enum ScratchSlot {
     kScratchSum = 1,
     kScratchLayerNorm = 2,
     kScratchColSum = 3,
-    kScratchSlots = 4
+    kScratchGemmSplit = 4,
+    kScratchSlots = 5
 };
 
 }  // namespace ember

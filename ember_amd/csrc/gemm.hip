@@ -4,6 +4,10 @@
 //   matmul(a, b, out, n, m, k):          out(n x m) = a(n x k) @ b(k x m)
 //   matmul_batched(..., batch, n, m, k): the same per batch with strides
 //                                        n*k, k*m, n*m
+// and adds gemm_ex, which also takes either operand transposed in place
+// (a stored k x n, b stored m x k: the weight- and input-gradient products of
+// a Linear layer, ember/nn/layers.py:50-56, without materialising T(x)) and
+// the fused epilogue of linear_fwd.
 // all row-major fp32 with fp32 accumulation (v_mfma_f32_32x32x2f32; no
 // reduced-precision inputs).  The CPU path of the reference accumulates in
 // double (src/tensor/operators_cpu.c:47-60); agreement is to fp32 rounding
@@ -34,8 +38,12 @@ struct GemmArgs {
     const float *a, *b;
     float *c;
     int n, m, k;
+    int lda, ldb;        // row pitch of a and b as stored (k or n; m or k)
+    int ta, tb;          // a stored k x n / b stored m x k
     int64_t sa, sb, sc;  // batch strides (elements)
     int tiles_n, tiles_m;
+    int kchunk;          // split-K: k range of one blockIdx.z (multiple of 16)
+    float *part;         // split-K partial sums [ksplit][batch][n][m]
     // Epilogue (all optional): out = act(acc + bias[col]) + residual, with
     // pre = acc + bias stored before the activation; residual and pre use
     // out's layout and batch stride.
@@ -80,12 +88,14 @@ __device__ __forceinline__ void load_slab(const GemmArgs &g, const float *A, con
             const int r = idx >> 3, c4 = idx & 7;
             const int row = row0 + r, col = k0 + 4 * c4;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (VEC) {
-                if (row < g.n && col < g.k) v = *(const f32x4 *)(A + (int64_t)row * g.k + col);
+            if (VEC && !g.ta) {
+                if (row < g.n && col < g.k) v = *(const f32x4 *)(A + (int64_t)row * g.lda + col);
             } else if (row < g.n) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    if (col + j < g.k) v[j] = A[(int64_t)row * g.k + col + j];
+                    if (col + j < g.k)
+                        v[j] = g.ta ? A[(int64_t)(col + j) * g.lda + row]
+                                    : A[(int64_t)row * g.lda + col + j];
             }
             ra[it] = v;
         }
@@ -93,12 +103,14 @@ __device__ __forceinline__ void load_slab(const GemmArgs &g, const float *A, con
             const int r = idx >> 5, c4 = idx & 31;
             const int row = k0 + r, col = col0 + 4 * c4;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (VEC) {
-                if (row < g.k && col < g.m) v = *(const f32x4 *)(B + (int64_t)row * g.m + col);
+            if (VEC && !g.tb) {
+                if (row < g.k && col < g.m) v = *(const f32x4 *)(B + (int64_t)row * g.ldb + col);
             } else if (row < g.k) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    if (col + j < g.m) v[j] = B[(int64_t)row * g.m + col + j];
+                    if (col + j < g.m)
+                        v[j] = g.tb ? B[(int64_t)(col + j) * g.ldb + row]
+                                    : B[(int64_t)row * g.ldb + col + j];
             }
             rb[it] = v;
         }
@@ -218,28 +230,44 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(GemmArgs g)
 //   * k is walked in slabs of 16, copied HBM -> LDS directly
 //     (global_load_lds_dwordx4, no registers) one slab ahead into the
 //     other of two buffers; one barrier per slab.
-//   * A slab (128 x 16) sits in rows padded to 20 floats: the A operand
-//     (16 rows at one column per lane group) then hits 16 different bank
-//     groups.  B slab (16 x 256) is unpadded: a lane reads 4 consecutive
+//   * A slab, a stored n x k: 128 tile rows padded to 20 floats, so the A
+//     operand (one row per lane, 4 k per ds_read_b128) hits 16 different
+//     bank groups.  a stored k x n (TA): 16 k-rows of 128 floats; a lane
+//     reads two neighbouring tile rows with one ds_read_b64 and uses them as
+//     the two row blocks of its wave, i.e. MFMA row r of row block rb is tile
+//     row 2r + rb of the wave's 64 (undone in the store).
+//   * B slab, b stored k x m: 16 rows of 256, a lane reads 4 consecutive
 //     columns with one ds_read_b128, one per accumulator column block
-//     (column = 4*lane + cb), so each B read feeds 8 MFMAs and each A read 16.
+//     (column = 4*lane + cb).  b stored m x k (TB): 256 columns padded to 20
+//     floats, a lane reads 4 k of its column with one ds_read_b128 (column =
+//     32*cb + lane).  Either way each B read feeds 8 MFMAs.
 //   * every LDS address in the loop is a per-lane base plus a compile-time
 //     offset.
 //   * tiles are numbered so that the tiles one XCD runs (workgroup ids are
 //     dealt to the 8 XCDs round-robin) are contiguous, and within that
 //     range grouped 8 row tiles per B column panel for L2 reuse.
+//   * split-K (SPLIT): blockIdx.z walks k in [z*kchunk, (z+1)*kchunk) and
+//     stores its raw sums to part; gemm_splitk_reduce adds the splits in
+//     order and applies the epilogue, so results do not depend on timing.
 constexpr int FM = 128, FN = 256, FK = 16;
-constexpr int FASTR = FK + 4;                 // padded A row
-constexpr int FA_CHUNKS = FM * (FASTR / 4);   // 16-byte chunks per A slab (640)
-constexpr int FA_DMA = FA_CHUNKS / 64;        // 1 KiB copies per A slab (10)
-constexpr int FB_DMA = FK;                    // one 1 KiB copy per B row (16)
-constexpr int FA_BUF = FM * FASTR;            // floats
-constexpr int FB_BUF = FK * FN;
+constexpr int FASTR = FK + 4;  // padded row of a k-contiguous slab
 
+template <bool TA> struct ASlab {
+    static constexpr int kBuf = TA ? FK * FM : FM * FASTR;     // floats
+    static constexpr int kCopies = TA ? kBuf / 256 : kBuf / 256;  // 1 KiB copies: 8 / 10
+};
+template <bool TB> struct BSlab {
+    static constexpr int kBuf = TB ? FN * FASTR : FK * FN;
+    static constexpr int kCopies = kBuf / 256;                  // 20 / 16
+};
+
+template <bool TA, bool TB, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
 {
-    __shared__ float As0[FA_BUF], As1[FA_BUF];
-    __shared__ float Bs0[FB_BUF], Bs1[FB_BUF];
+    constexpr int ABUF = ASlab<TA>::kBuf, BBUF_ = BSlab<TB>::kBuf;
+    constexpr int ACOP = ASlab<TA>::kCopies, BCOP = BSlab<TB>::kCopies;
+    __shared__ float As0[ABUF], As1[ABUF];
+    __shared__ float Bs0[BBUF_], Bs1[BBUF_];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -259,31 +287,51 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
     const int in_grp = tile - grp * per_group;
     const int row0 = (first + in_grp % rows_in_grp) * FM;
     const int col0 = (in_grp / rows_in_grp) * FN;
-    const float *A = g.a + (int64_t)blockIdx.y * g.sa + (int64_t)row0 * g.k;
-    const float *B = g.b + (int64_t)blockIdx.y * g.sb + col0;
-    float *C = g.c + (int64_t)blockIdx.y * g.sc + (int64_t)row0 * g.m + col0;
 
-    // This lane's chunk of each A copy it issues (t = w, w+4, w+8 < 10):
-    // row p / 5, chunk p % 5 (chunk 4 is row padding: re-read chunk 0).
-    unsigned aoff[3];
-#pragma unroll
-    for (int s = 0; s < 3; ++s) {
-        const int p = 64 * (w + 4 * s) + lane;
-        const int r = p / (FASTR / 4);
-        const int c = p - r * (FASTR / 4);
-        aoff[s] = (unsigned)(r * g.k + 4 * (c < 4 ? c : 0));
+    int kbeg = 0, kend = g.k;
+    if (SPLIT) {
+        kbeg = blockIdx.z * g.kchunk;
+        kend = min(g.k, kbeg + g.kchunk);
     }
-    const unsigned boff = (unsigned)(4 * lane);
+    // Tile origins; slab k0 (absolute) is added per fetch.
+    const float *A = g.a + (int64_t)blockIdx.y * g.sa + (TA ? (int64_t)row0 : (int64_t)row0 * g.lda);
+    const float *B = g.b + (int64_t)blockIdx.y * g.sb + (TB ? (int64_t)col0 * g.ldb : (int64_t)col0);
+
+    // Per-lane offsets of the 1 KiB copies this wave issues (copy t = w + 4s).
+    constexpr int AS = (ACOP + 3) / 4, BS = (BCOP + 3) / 4;
+    unsigned aoff[AS], boff[BS];
+#pragma unroll
+    for (int s = 0; s < AS; ++s) {
+        const int t = w + 4 * s;
+        if (TA) {  // copy t: k-rows 2t, 2t+1, 32 chunks each
+            aoff[s] = (unsigned)((2 * t + h32) * g.lda + 4 * l32);
+        } else {   // row p / 5, chunk p % 5 (chunk 4 is row padding: re-read chunk 0)
+            const int p = 64 * t + lane;
+            const int r = p / (FASTR / 4), c = p - r * (FASTR / 4);
+            aoff[s] = (unsigned)(r * g.lda + 4 * (c < 4 ? c : 0));
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < BS; ++s) {
+        const int t = w + 4 * s;
+        if (TB) {
+            const int p = 64 * t + lane;
+            const int r = p / (FASTR / 4), c = p - r * (FASTR / 4);
+            boff[s] = (unsigned)(r * g.ldb + 4 * (c < 4 ? c : 0));
+        } else {   // copy t: k-row t
+            boff[s] = (unsigned)(t * g.ldb + 4 * lane);
+        }
+    }
 
     auto fetch = [&](int k0, float *__restrict__ as, float *__restrict__ bs) {
+        const float *Ak = TA ? A + (int64_t)k0 * g.lda : A + k0;
+        const float *Bk = TB ? B + k0 : B + (int64_t)k0 * g.ldb;
 #pragma unroll
-        for (int s = 0; s < 3; ++s)
-            if (w + 4 * s < FA_DMA) dma16(A + k0 + aoff[s], as + 256 * (w + 4 * s));
+        for (int s = 0; s < AS; ++s)
+            if (w + 4 * s < ACOP) dma16(Ak + aoff[s], as + 256 * (w + 4 * s));
 #pragma unroll
-        for (int s = 0; s < FB_DMA / 4; ++s) {
-            const int r = w + 4 * s;
-            dma16(B + (int64_t)(k0 + r) * g.m + boff, bs + 256 * r);
-        }
+        for (int s = 0; s < BS; ++s)
+            if (w + 4 * s < BCOP) dma16(Bk + boff[s], bs + 256 * (w + 4 * s));
     };
 
     f32x16 acc[2][4];
@@ -292,17 +340,37 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
 
-    const int abase = (64 * wr + l32) * FASTR + 8 * h32;
-    const int bbase = 8 * h32 * FN + 128 * wc + 4 * l32;
+    const int abase = TA ? 8 * h32 * FM + 64 * wr + 2 * l32 : (64 * wr + l32) * FASTR + 8 * h32;
+    const int bbase = TB ? (128 * wc + l32) * FASTR + 8 * h32 : 8 * h32 * FN + 128 * wc + 4 * l32;
     auto slab = [&](const float *__restrict__ as, const float *__restrict__ bs) {
 #pragma unroll
         for (int kk = 0; kk < 8; kk += 4) {
             f32x4 af[2];
+            if (TA) {
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) af[rb] = *(const f32x4 *)&as[abase + rb * 32 * FASTR + kk];
+                for (int j = 0; j < 4; ++j) {
+                    const f32x2 v = *(const f32x2 *)&as[abase + (kk + j) * FM];
+                    af[0][j] = v[0];
+                    af[1][j] = v[1];
+                }
+            } else {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) af[rb] = *(const f32x4 *)&as[abase + rb * 32 * FASTR + kk];
+            }
+            f32x4 bt[4];
+            if (TB) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) bt[cb] = *(const f32x4 *)&bs[bbase + cb * 32 * FASTR + kk];
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const f32x4 bf = *(const f32x4 *)&bs[bbase + (kk + j) * FN];
+                f32x4 bf;
+                if (TB) {
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) bf[cb] = bt[cb][j];
+                } else {
+                    bf = *(const f32x4 *)&bs[bbase + (kk + j) * FN];
+                }
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -311,50 +379,116 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
         }
     };
 
-    const int nslab = g.k / FK;
-    fetch(0, As0, Bs0);
-    wait_vmem();
-    __syncthreads();
+    const int nslab = (kend - kbeg) / FK;
+    if (nslab > 0) {
+        fetch(kbeg, As0, Bs0);
+        wait_vmem();
+        __syncthreads();
+    }
     // Two slabs per trip so that each buffer is a distinct LDS object: the
     // compiler then knows the copy into one does not feed reads of the other.
     for (int s = 0; s < nslab; s += 2) {
-        if (s + 1 < nslab) fetch((s + 1) * FK, As1, Bs1);
+        if (s + 1 < nslab) fetch(kbeg + (s + 1) * FK, As1, Bs1);
         slab(As0, Bs0);
         wait_vmem();
         __syncthreads();
         if (s + 1 < nslab) {
-            if (s + 2 < nslab) fetch((s + 2) * FK, As0, Bs0);
+            if (s + 2 < nslab) fetch(kbeg + (s + 2) * FK, As0, Bs0);
             slab(As1, Bs1);
             wait_vmem();
             __syncthreads();
         }
     }
 
+    // Output: row(rb, i) and col(cb) as the operand layouts above define them.
+    const int64_t zoff = SPLIT ? ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * g.sc
+                               : (int64_t)blockIdx.y * g.sc;
+    float *C = (SPLIT ? g.part : g.c) + zoff + (int64_t)row0 * g.m + col0;
+    const bool epi = !SPLIT && (g.bias || g.pre || g.act || g.residual);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int row = 64 * wr + 32 * rb + acc_row(i, h32);
+            const int row = TA ? 64 * wr + 2 * acc_row(i, h32) + rb : 64 * wr + 32 * rb + acc_row(i, h32);
             f32x4 v;
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) v[cb] = acc[rb][cb][i];
-            if (g.bias || g.pre || g.act || g.residual) {
-                const int col = col0 + 128 * wc + 4 * l32;
-                const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)(row0 + row) * g.m + col;
+            if (TB) {
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) v[cb] = epilogue(g, v[cb], off + cb, col + cb);
+                for (int cb = 0; cb < 4; ++cb) {
+                    const int col = 128 * wc + 32 * cb + l32;
+                    float x = v[cb];
+                    if (epi) {
+                        const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)(row0 + row) * g.m + col0 + col;
+                        x = epilogue(g, x, off, col0 + col);
+                    }
+                    C[(int64_t)row * g.m + col] = x;
+                }
+            } else {
+                const int col = 128 * wc + 4 * l32;
+                if (epi) {
+                    const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)(row0 + row) * g.m + col0 + col;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) v[cb] = epilogue(g, v[cb], off + cb, col0 + col + cb);
+                }
+                *(f32x4 *)&C[(int64_t)row * g.m + col] = v;
             }
-            *(f32x4 *)&C[(int64_t)row * g.m + 128 * wc + 4 * l32] = v;
         }
     }
 }
 
+// out = epilogue(sum over z of part[z]), z in order; m % 4 == 0.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmArgs g, int ksplit, int64_t total)
+{
+    const int64_t n4 = total / 4;
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n4; q += (int64_t)gridDim.x * 256) {
+        const int64_t off = 4 * q;
+        f32x4 s = *(const f32x4 *)&g.part[off];
+        for (int z = 1; z < ksplit; ++z) {
+            const f32x4 v = *(const f32x4 *)&g.part[(int64_t)z * total + off];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] += v[c];
+        }
+        if (g.bias || g.pre || g.act || g.residual) {
+            const int col = (int)(off % g.m);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] = epilogue(g, s[c], off + c, col + c);
+        }
+        *(f32x4 *)&g.c[off] = s;
+    }
+}
+
+int g_num_cus[16];
+
+int num_cus()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (g_num_cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        g_num_cus[dev] = n;
+    }
+    return g_num_cus[dev];
+}
+
+template <bool TA, bool TB>
+void launch_fast(const GemmArgs &g, dim3 grid, bool split)
+{
+    if (split)
+        hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, true>), grid, dim3(kThreads), 0, 0, g);
+    else
+        hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, false>), grid, dim3(kThreads), 0, 0, g);
+}
+
 int gemm_launch(const float *a, const float *b, float *out, int batch, int n, int m, int k,
                 const char *who, const float *bias = nullptr, const float *residual = nullptr,
-                float *pre = nullptr, int act = 0)
+                float *pre = nullptr, int act = 0, int ta = 0, int tb = 0)
 {
     if (n < 0 || m < 0 || k < 0 || batch < 0) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     if ((int64_t)n * m == 0 || batch == 0) return EMBER_OK;
+    if (!a || !b || !out) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     GemmArgs g;
     g.a = a;
     g.b = b;
@@ -362,23 +496,61 @@ int gemm_launch(const float *a, const float *b, float *out, int batch, int n, in
     g.n = n;
     g.m = m;
     g.k = k;
+    g.ta = ta;
+    g.tb = tb;
+    g.lda = ta ? n : k;
+    g.ldb = tb ? k : m;
     g.sa = (int64_t)n * k;
     g.sb = (int64_t)k * m;
     g.sc = (int64_t)n * m;
     g.tiles_n = (n + BM - 1) / BM;
     g.tiles_m = (m + BN - 1) / BN;
+    g.kchunk = k;
+    g.part = nullptr;
     g.bias = bias;
     g.residual = residual;
     g.pre = pre;
     g.act = act;
     if (batch > 65535) return record_error(EMBER_ERR_UNSUPPORTED, who);
-    const bool vec = (k % 4 == 0) && (m % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
+    const bool vec = (k % 4 == 0) && (m % 4 == 0) && (n % 4 == 0 || !ta) &&
+                     (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
     if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 && ((uintptr_t)out % 16) == 0) {
         g.tiles_n = n / FM;
         g.tiles_m = m / FN;
-        hipLaunchKernelGGL(gemm_f32_dma_kernel, dim3(g.tiles_n * g.tiles_m, batch), dim3(kThreads),
-                           0, 0, g);
-        return launch_ok(who) ? EMBER_OK : EMBER_ERR_DEVICE;
+        const int work = g.tiles_n * g.tiles_m * batch;
+        // Fewer tiles than CUs: split k so that about two workgroups run per
+        // CU, each over at least 512 of k.
+        int ksplit = 1;
+        const int cus = num_cus();
+        if (work < cus && k >= 1024) {
+            ksplit = min(2 * cus / work, k / 512);
+            if (ksplit > 64) ksplit = 64;
+            if (ksplit > 1) {
+                g.kchunk = ((k + ksplit - 1) / ksplit + FK - 1) / FK * FK;
+                ksplit = (k + g.kchunk - 1) / g.kchunk;
+            }
+        }
+        dim3 grid(g.tiles_n * g.tiles_m, batch, ksplit);
+        const bool split = ksplit > 1;
+        if (split) {
+            const int64_t total = (int64_t)batch * n * m;
+            g.part = (float *)scratch(kScratchGemmSplit, (size_t)ksplit * total * sizeof(float));
+            if (!g.part) return EMBER_ERR_OUT_OF_MEMORY;
+        }
+        if (ta)
+            tb ? launch_fast<true, true>(g, grid, split) : launch_fast<true, false>(g, grid, split);
+        else
+            tb ? launch_fast<false, true>(g, grid, split) : launch_fast<false, false>(g, grid, split);
+        if (!launch_ok(who)) return EMBER_ERR_DEVICE;
+        if (split) {
+            const int64_t total = (int64_t)batch * n * m;
+            int64_t blocks = (total / 4 + 255) / 256;
+            if (blocks > 8 * cus) blocks = 8 * cus;
+            hipLaunchKernelGGL(gemm_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, 0, g,
+                               ksplit, total);
+            if (!launch_ok("gemm_splitk_reduce")) return EMBER_ERR_DEVICE;
+        }
+        return EMBER_OK;
     }
     const dim3 grid(g.tiles_n * g.tiles_m, batch);
     if (vec)
@@ -408,6 +580,15 @@ int linear_fwd(const float *a, const float *b, const float *bias, const float *r
 {
     if (act < 0 || act > 1) return ember::record_error(EMBER_ERR_INVALID_ARGUMENT, "linear_fwd");
     return ember::gemm_launch(a, b, out, 1, n, m, k, "linear_fwd", bias, residual, pre, act);
+}
+
+int gemm_ex(const float *a, const float *b, float *out, int batch, int n, int m, int k,
+            int trans_a, int trans_b, const float *bias, const float *residual, float *pre, int act)
+{
+    if (act < 0 || act > 1 || (trans_a != 0 && trans_a != 1) || (trans_b != 0 && trans_b != 1))
+        return ember::record_error(EMBER_ERR_INVALID_ARGUMENT, "gemm_ex");
+    return ember::gemm_launch(a, b, out, batch, n, m, k, "gemm_ex", bias, residual, pre, act,
+                              trans_a, trans_b);
 }
 
 }  // extern "C"

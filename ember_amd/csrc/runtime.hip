@@ -4,9 +4,29 @@
 // cudaFree / cudaMemcpy / cudaDeviceSynchronize) and the exit()-on-error
 // macros of src/core/utils_gpu.cuh:8-34 with HIP calls whose failures are
 // recorded and reported instead of terminating the process.
+//
+// alloc_memory / free_memory keep a per-device cache of freed blocks.  The
+// reference's free_memory is cudaFree, which waits for the whole device, and
+// its alloc_memory a cudaMalloc per tensor; a training step of a small model
+// frees and allocates hundreds of tensors, so the host stalled on every free
+// and the queue of launches drained.  Here a freed block goes back to the
+// cache at once and the next allocation of a similar size reuses it.  This
+// is safe because every kernel and copy of the library is enqueued on the
+// HIP null stream, which runs in order: work enqueued after the reuse cannot
+// start before work enqueued before the free has finished.  (Memory used by
+// work on other streams must be synchronised by its user before it is freed,
+// as with any stream-ordered allocator.)  Sizes are rounded to 512 B below
+// 1 MiB and to 2 MiB above; a cached block is reused for a request of up to
+// 1.25 x smaller.  When hipMalloc runs out of memory the device's cache is
+// released (after a device synchronisation) and the allocation retried.
+// EMBER_AMD_NO_CACHE=1 in the environment turns the cache off (plain
+// hipMalloc / hipFree per call, the reference's behaviour).
 #include <stdio.h>
+#include <stdlib.h>
 
+#include <map>
 #include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -74,6 +94,112 @@ void *scratch(int slot, size_t bytes)
     return p;
 }
 
+namespace {
+
+struct LiveBlock {
+    size_t bytes;  // rounded size of the hipMalloc'd block
+    int dev;
+};
+
+struct DevicePool {
+    std::multimap<size_t, void *> free_blocks;  // rounded size -> block
+    size_t cached = 0;                          // bytes held in free_blocks
+    size_t in_use = 0;                          // bytes handed out
+    size_t peak = 0;                            // max of in_use
+};
+
+std::mutex g_alloc_mu;
+std::unordered_map<void *, LiveBlock> g_live;  // blocks handed out by alloc_memory
+DevicePool g_pool[kMaxDevices];
+int g_cache_mode = -1;                         // -1 unresolved, 0 off, 1 on
+
+bool cache_on()
+{
+    if (g_cache_mode < 0) {
+        const char *v = getenv("EMBER_AMD_NO_CACHE");
+        g_cache_mode = (v && v[0] && !(v[0] == '0' && v[1] == 0)) ? 0 : 1;
+    }
+    return g_cache_mode == 1;
+}
+
+size_t round_bytes(size_t b)
+{
+    constexpr size_t kSmall = 512, kLarge = size_t(2) << 20;
+    if (b < (size_t(1) << 20)) return (b + kSmall - 1) / kSmall * kSmall;
+    return (b + kLarge - 1) / kLarge * kLarge;
+}
+
+// Returns every cached block of `dev` to HIP.  Caller holds g_alloc_mu and
+// has made `dev` current.
+void release_cached(int dev)
+{
+    DevicePool &p = g_pool[dev];
+    if (p.free_blocks.empty()) return;
+    // Freed blocks may still be read by queued work.
+    hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize(empty_cache)");
+    for (auto &kv : p.free_blocks) hip_ok(hipFree(kv.second), "hipFree(empty_cache)");
+    p.free_blocks.clear();
+    p.cached = 0;
+}
+
+void *cached_alloc(size_t bytes)
+{
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= kMaxDevices) {
+        record_error(EMBER_ERR_UNSUPPORTED, "alloc_memory: device index");
+        return nullptr;
+    }
+    const size_t want = round_bytes(bytes);
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    DevicePool &p = g_pool[dev];
+    void *ptr = nullptr;
+    size_t got = want;
+    auto it = p.free_blocks.lower_bound(want);
+    if (it != p.free_blocks.end() && it->first <= want + want / 4) {
+        ptr = it->second;
+        got = it->first;
+        p.cached -= got;
+        p.free_blocks.erase(it);
+    } else {
+        hipError_t err = hipMalloc(&ptr, want);
+        if (err == hipErrorOutOfMemory && !p.free_blocks.empty()) {
+            (void)hipGetLastError();
+            release_cached(dev);
+            err = hipMalloc(&ptr, want);
+        }
+        if (err != hipSuccess) {
+            // Same contract as memory_gpu.cu:15-19: report and return NULL;
+            // the binding turns NULL into MemoryError.
+            record_error(EMBER_ERR_OUT_OF_MEMORY, "alloc_memory", err);
+            (void)hipGetLastError();
+            return nullptr;
+        }
+    }
+    g_live.emplace(ptr, LiveBlock{got, dev});
+    p.in_use += got;
+    if (p.in_use > p.peak) p.peak = p.in_use;
+    return ptr;
+}
+
+void cached_free(void *ptr)
+{
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    auto it = g_live.find(ptr);
+    if (it == g_live.end()) {
+        // Not from alloc_memory (e.g. memory hipMalloc'd by the caller).
+        hip_ok(hipFree(ptr), "free_memory");
+        return;
+    }
+    DevicePool &p = g_pool[it->second.dev];
+    p.in_use -= it->second.bytes;
+    p.cached += it->second.bytes;
+    p.free_blocks.emplace(it->second.bytes, ptr);
+    g_live.erase(it);
+}
+
+}  // namespace
+
 }  // namespace ember
 
 extern "C" {
@@ -99,6 +225,8 @@ const char *ember_error_string(int status)
 
 void *alloc_memory(size_t bytes)
 {
+    if (bytes == 0) return nullptr;  // hipMalloc(0) gives NULL without error
+    if (ember::cache_on()) return ember::cached_alloc(bytes);
     void *ptr = nullptr;
     hipError_t err = hipMalloc(&ptr, bytes);
     if (err != hipSuccess) {
@@ -113,7 +241,34 @@ void *alloc_memory(size_t bytes)
 
 void free_memory(void *ptr)
 {
-    if (ptr) ember::hip_ok(hipFree(ptr), "free_memory");
+    if (!ptr) return;
+    if (ember::cache_on())
+        ember::cached_free(ptr);
+    else
+        ember::hip_ok(hipFree(ptr), "free_memory");
+}
+
+void ember_empty_cache(void)
+{
+    int dev = 0;
+    if (!ember::hip_ok(hipGetDevice(&dev), "hipGetDevice")) return;
+    std::lock_guard<std::mutex> lock(ember::g_alloc_mu);
+    if (dev >= 0 && dev < ember::kMaxDevices) ember::release_cached(dev);
+}
+
+void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak)
+{
+    int dev = 0;
+    size_t u = 0, c = 0, pk = 0;
+    if (ember::hip_ok(hipGetDevice(&dev), "hipGetDevice") && dev >= 0 && dev < ember::kMaxDevices) {
+        std::lock_guard<std::mutex> lock(ember::g_alloc_mu);
+        u = ember::g_pool[dev].in_use;
+        c = ember::g_pool[dev].cached;
+        pk = ember::g_pool[dev].peak;
+    }
+    if (in_use) *in_use = u;
+    if (cached) *cached = c;
+    if (peak) *peak = pk;
 }
 
 void copy_to_device(void *dst_device, const void *src_host, size_t bytes)

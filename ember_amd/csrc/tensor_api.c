@@ -674,6 +674,37 @@ static PyObject *py_linear(PyObject *module, PyObject *args)
     return Py_BuildValue("(NN)", (PyObject *)y, (PyObject *)pre);
 }
 
+/* _gemm(a, b, batch, n, m, k, trans_a, trans_b, bias|None, residual|None) -> out:
+ * out = op(a) @ op(b) + bias + residual per batch, op(a) = a (n x k) or a^T
+ * of a stored (k x n), op(b) = b (k x m) or b^T of b stored (m x k). */
+static PyObject *py_gemm(PyObject *module, PyObject *args)
+{
+    TensorObject *a, *b;
+    PyObject *bo, *ro;
+    int batch, n, m, k, ta, tb;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!iiiippOO", &TensorType, &a, &TensorType, &b, &batch, &n, &m,
+                          &k, &ta, &tb, &bo, &ro))
+        return NULL;
+    TensorObject *bias = opt_tensor(bo, "bias"), *res = opt_tensor(ro, "residual");
+    if (bias == (TensorObject *)-1 || res == (TensorObject *)-1) return NULL;
+    if (batch < 0 || n < 0 || m < 0 || k < 0 || a->size != (Py_ssize_t)batch * n * k ||
+        b->size != (Py_ssize_t)batch * k * m || (bias && bias->size != m) ||
+        (res && res->size != (Py_ssize_t)batch * n * m)) {
+        PyErr_SetString(PyExc_ValueError, "_gemm: operand sizes do not match (batch, n, m, k)");
+        return NULL;
+    }
+    TensorObject *out = alloc_tensor((Py_ssize_t)batch * n * m);
+    if (!out) return NULL;
+    int st = gemm_ex(a->d_ptr, b->d_ptr, out->d_ptr, batch, n, m, k, ta, tb,
+                     bias ? bias->d_ptr : NULL, res ? res->d_ptr : NULL, NULL, 0);
+    if (raise_status(st, "_gemm")) {
+        Py_DECREF(out);
+        return NULL;
+    }
+    return (PyObject *)out;
+}
+
 static PyObject *py_gelu_bwd(PyObject *module, PyObject *args)
 {
     TensorObject *dy, *u, *y;
@@ -898,6 +929,26 @@ static PyObject *py_synchronize(PyObject *module, PyObject *unused)
     Py_RETURN_NONE;
 }
 
+static PyObject *py_empty_cache(PyObject *module, PyObject *unused)
+{
+    (void)module;
+    (void)unused;
+    ember_empty_cache();
+    if (raise_status(0, "_empty_cache")) return NULL;
+    Py_RETURN_NONE;
+}
+
+static PyObject *py_memory_stats(PyObject *module, PyObject *unused)
+{
+    (void)module;
+    (void)unused;
+    size_t in_use = 0, cached = 0, peak = 0;
+    ember_memory_stats(&in_use, &cached, &peak);
+    if (raise_status(0, "_memory_stats")) return NULL;
+    return Py_BuildValue("{s:K,s:K,s:K}", "in_use", (unsigned long long)in_use, "cached",
+                         (unsigned long long)cached, "peak", (unsigned long long)peak);
+}
+
 /* ---- module ---- */
 
 #define METHOD(pyname, fn, doc) {pyname, (PyCFunction)fn, METH_VARARGS, doc}
@@ -919,6 +970,7 @@ static PyMethodDef module_methods[] = {
     METHOD("_attention_bwd", py_attention_bwd, "fused attention backward -> (dq, dk, dv)"),
     METHOD("_adam_step", py_adam_step, "fused Adam step over lists of _Tensor, in place"),
     METHOD("_linear", py_linear, "act(x @ w + bias) + residual -> (y, pre)"),
+    METHOD("_gemm", py_gemm, "op(a) @ op(b) + bias + residual with either operand transposed in place"),
     METHOD("_gelu_bwd", py_gelu_bwd, "backward of Ember's GELU"),
     METHOD("_col_sum", py_col_sum, "column sums (bias gradient)"),
     METHOD("_layernorm_fwd", py_layernorm_fwd, "LayerNorm -> (y, mean, rstd)"),
@@ -926,6 +978,10 @@ static PyMethodDef module_methods[] = {
     METHOD("_attention_fwd_packed", py_attention_fwd_packed, "attention on packed (B,S,3,H,D) qkv"),
     METHOD("_attention_bwd_packed", py_attention_bwd_packed, "backward -> packed dqkv"),
     {"_synchronize", (PyCFunction)py_synchronize, METH_NOARGS, "wait for all queued device work"},
+    {"_empty_cache", (PyCFunction)py_empty_cache, METH_NOARGS,
+     "return the allocator's cached blocks on the current device to HIP"},
+    {"_memory_stats", (PyCFunction)py_memory_stats, METH_NOARGS,
+     "allocator bytes in use, cached and peak in use on the current device"},
     {NULL, NULL, 0, NULL}};
 
 static PyModuleDef tensor_module = {

@@ -20,7 +20,7 @@ from itertools import chain
 
 from ember_amd import _core as C
 from ember_amd import random as _random
-from ember_amd.tensor import T, Tensor, attention_backward, attention_forward
+from ember_amd.tensor import Tensor, attention_backward, attention_forward
 
 
 class Layer(ABC):
@@ -130,6 +130,29 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None = None, residual: Tensor | Non
     return Tensor._from_core(y, (n, m)), (Tensor._from_core(pre, (n, m)) if pre is not None else None)
 
 
+def weight_grad(x: Tensor, grad_y: Tensor) -> Tensor:
+    """x^T @ grad_y (in x out) for x (rows, in), grad_y (rows, out), reading x
+    transposed in place (Ember's ``em.T(x) @ grad_y``, ``layers.py:53``)."""
+    rows, n = _rows(x)
+    rows2, m = _rows(grad_y)
+    if rows != rows2:
+        raise ValueError(f"Shape mismatch: {x.shape} and {grad_y.shape}")
+    return Tensor._from_core(C._gemm(x._core, grad_y._core, 1, n, m, rows, True, False, None, None),
+                             (n, m))
+
+
+def input_grad(grad_y: Tensor, w: Tensor, residual: Tensor | None = None) -> Tensor:
+    """grad_y @ w^T (+ residual) for w (in, out), reading w transposed in place
+    (Ember's ``grad_y @ em.T(self.w)``, ``layers.py:55``)."""
+    rows, m_out = _rows(grad_y)
+    n_in, m_out2 = _rows(w)
+    if m_out != m_out2:
+        raise ValueError(f"Shape mismatch: {grad_y.shape} and {w.shape}")
+    return Tensor._from_core(
+        C._gemm(grad_y._core, w._core, 1, rows, n_in, m_out, False, True, None,
+                None if residual is None else residual._core), (rows, n_in))
+
+
 def col_sum(x: Tensor) -> Tensor:
     """Column sums of a 2-D Tensor (a Linear layer's bias gradient)."""
     n, m = _rows(x)
@@ -173,9 +196,9 @@ class Linear(Layer):
         if self.activation == "gelu":
             grad_y = Tensor._from_core(C._gelu_bwd(grad_y._core, self.pre._core, self.y._core),
                                        grad_y.shape)
-        self.grad_w = T(self.x) @ grad_y
+        self.grad_w = weight_grad(self.x, grad_y)
         self.grad_b = col_sum(grad_y)
-        return grad_y @ T(self.w)
+        return input_grad(grad_y, self.w)
 
 
 class GELU(Layer):
@@ -308,19 +331,19 @@ class DecoderBlock(Layer):
         B, S, scale, h1, qkv, o, lse, x2, h2, a, u = self._saved
         D = self.d // self.h
         # MLP: y = x2 + GELU(h2 W1 + b1) W2 + b2
-        g_w2, g_b2 = T(a) @ grad_y, col_sum(grad_y)
-        da = grad_y @ T(self.w_2)
+        g_w2, g_b2 = weight_grad(a, grad_y), col_sum(grad_y)
+        da = input_grad(grad_y, self.w_2)
         du = Tensor._from_core(C._gelu_bwd(da._core, u._core, a._core), da.shape)
-        g_w1, g_b1 = T(h2) @ du, col_sum(du)
-        dx2 = self.ln2.backward(du @ T(self.w_1)) + grad_y
+        g_w1, g_b1 = weight_grad(h2, du), col_sum(du)
+        dx2 = self.ln2.backward(input_grad(du, self.w_1)) + grad_y
         # attention: x2 = x + O Wo + bo
-        g_wo, g_bo = T(o) @ dx2, col_sum(dx2)
-        d_o = dx2 @ T(self.w_o)
+        g_wo, g_bo = weight_grad(o, dx2), col_sum(dx2)
+        d_o = input_grad(dx2, self.w_o)
         dqkv = Tensor._from_core(
             C._attention_bwd_packed(qkv._core, o._core, lse, d_o._core, B, S, self.h, D, scale,
                                     self.causal), qkv.shape)
-        g_wqkv, g_bqkv = T(h1) @ dqkv, col_sum(dqkv)
-        dx = self.ln1.backward(dqkv @ T(self.w_qkv)) + dx2
+        g_wqkv, g_bqkv = weight_grad(h1, dqkv), col_sum(dqkv)
+        dx = self.ln1.backward(input_grad(dqkv, self.w_qkv)) + dx2
         self._grads = [self.ln1.grad_gamma, self.ln1.grad_beta, g_wqkv, g_bqkv, g_wo, g_bo,
                        self.ln2.grad_gamma, self.ln2.grad_beta, g_w1, g_b1, g_w2, g_b2]
         return dx

@@ -415,3 +415,15 @@ def attention_backward(q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, 
 def synchronize() -> None:
     """Waits for all queued device work."""
     C._synchronize()
+
+
+def empty_cache() -> None:
+    """Returns the device allocator's cached (freed) blocks to HIP; the next
+    allocations call hipMalloc again."""
+    C._empty_cache()
+
+
+def memory_stats() -> dict:
+    """Bytes the device allocator has handed out (``in_use``), holds freed for
+    reuse (``cached``) and the peak of ``in_use``, on the current device."""
+    return C._memory_stats()

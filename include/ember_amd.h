@@ -50,6 +50,16 @@ void free_memory(void *ptr);
 void copy_to_device(void *dst_device, const void *src_host, size_t bytes);
 void copy_from_device(void *dst_host, const void *src_device, size_t bytes);
 void sync_device(void);
+/* alloc_memory/free_memory cache freed blocks per device instead of calling
+ * hipFree (which synchronises the device) on every free; reuse is ordered by
+ * the null stream all library work runs on.  EMBER_AMD_NO_CACHE=1 turns the
+ * cache off.  No reference counterpart (memory_gpu.cu:10-28 calls
+ * cudaMalloc/cudaFree each time); these two report and release the cache.
+ * ember_empty_cache synchronises the current device and hipFrees every
+ * cached block; ember_memory_stats gives the current device's bytes handed
+ * out, bytes cached and peak bytes handed out (rounded block sizes). */
+void ember_empty_cache(void);
+void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak);
 
 /* ---- element-wise operators: replaces src/tensor/operators.h:10-18 ----
  * One declaration per row of ember_amd/csrc/operators.def, which lists the
@@ -148,6 +158,18 @@ int adam_step(float *const *params, const float *const *grads, float *const *exp
  * activation and the residual add as separate operators. */
 int linear_fwd(const float *a, const float *b, const float *bias, const float *residual,
                float *out, float *pre, int n, int m, int k, int act);
+
+/* out = act(op(a) @ op(b) + bias) + residual for `batch` products (strides
+ * n*k, k*m, n*m), where op(a) is a (n x k) or, with trans_a, the transpose of
+ * a stored (k x n), and op(b) is b (k x m) or, with trans_b, the transpose of
+ * b stored (m x k); pre as in linear_fwd.  Replaces Linear.backward's
+ * `em.T(x) @ grad_y` and `grad_y @ em.T(w)` (ember/nn/layers.py:50-56),
+ * which materialise the transposes, and generalises matmul /
+ * matmul_batched (operators_gpu.cu:114-136).  Products with fewer output
+ * tiles than CUs split k and add the parts in a fixed order (library
+ * scratch of splits * batch * n * m floats). */
+int gemm_ex(const float *a, const float *b, float *out, int batch, int n, int m, int k,
+            int trans_a, int trans_b, const float *bias, const float *residual, float *pre, int act);
 
 /* dx = dy * ((1 + tanh(0.8u)) * (0.5 + 0.8(u - y))): the backward of Ember's
  * GELU (ember/nn/activations.py:61-66) with u its input and y its output. */

@@ -70,6 +70,29 @@ def matmul_batched(a, b):
     return out.numpy()
 
 
+def gemm_ex(a, b, ta=False, tb=False, bias=None, residual=None, act=0):
+    """gemm_ex on stored operands: a is (k, n) when ta else (n, k), b is (m, k)
+    when tb else (k, m); leading batch dimensions allowed.  Returns out, and
+    pre as well when act is set."""
+    batch = a.shape[0] if a.ndim == 3 else 1
+    n, k = (a.shape[-1], a.shape[-2]) if ta else (a.shape[-2], a.shape[-1])
+    m = b.shape[-2] if tb else b.shape[-1]
+    say(f"gemm_ex batch={batch} n={n} m={m} k={k} ta={ta} tb={tb} act={act} "
+        f"bias={bias is not None} residual={residual is not None}")
+    da, db = DeviceArray.from_numpy(a), DeviceArray.from_numpy(b)
+    dbias = DeviceArray.from_numpy(bias) if bias is not None else None
+    dres = DeviceArray.from_numpy(residual) if residual is not None else None
+    shape = (batch, n, m) if a.ndim == 3 else (n, m)
+    out = DeviceArray(shape)
+    pre = DeviceArray(shape) if act else None
+    rc = capi.lib().gemm_ex(da.ptr, db.ptr, out.ptr, batch, n, m, k, int(ta), int(tb),
+                            None if dbias is None else dbias.ptr,
+                            None if dres is None else dres.ptr,
+                            None if pre is None else pre.ptr, act)
+    capi.check(rc, "gemm_ex")
+    return (out.numpy(), pre.numpy()) if act else out.numpy()
+
+
 def gemm_error_bound(a, b):
     """Rigorous bound on |fl(a@b) - a@b| for any fp32 summation order of
     length k: gamma_k * (|a| @ |b|), gamma_k = k u / (1 - k u), u = 2^-24,

@@ -87,3 +87,44 @@ def test_config4_shapes_sampled(n, k, m):
     rows = np.unique(np.concatenate([[0, 1, n - 1], np.random.default_rng(9).integers(0, n, 93)]))
     exact = oracle.matmul(a[rows], b, threads=True)
     _check(got[rows], a[rows], b, exact)
+
+
+def _stored(x, trans):
+    """The operand as gemm_ex reads it: its transpose, contiguous, if trans."""
+    return np.ascontiguousarray(np.swapaxes(x, -1, -2)) if trans else x
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize(
+    "n,k,m",
+    [(33, 17, 65), (100, 70, 90), (128, 16, 256), (256, 48, 512),      # unaligned / fast path
+     (128, 4096, 256), (1024, 8192, 1024), (256, 2048, 768),           # split-K: few tiles, long k
+     (384, 1040, 512), (1024, 1024, 3072)],                            # uneven split, no split
+)
+def test_gemm_ex_transposes_within_fp32_bound(n, k, m, ta, tb):
+    a, b = _u((n, k), n + k), _u((k, m), m + 1)
+    _check(G.gemm_ex(_stored(a, ta), _stored(b, tb), ta, tb), a, b)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, True)])
+def test_gemm_ex_batched_split(ta, tb):
+    a, b = _u((3, 128, 2048), 5), _u((3, 2048, 256), 6)
+    got = G.gemm_ex(_stored(a, ta), _stored(b, tb), ta, tb)
+    for i in range(3):
+        _check(got[i], a[i], b[i])
+
+
+@pytest.mark.parametrize("n,k,m", [(128, 4096, 256), (256, 64, 512), (70, 40, 30)])
+def test_gemm_ex_epilogue_with_and_without_split(n, k, m):
+    """bias + residual, and bias + GELU with pre, through the split-K reduction
+    (first shape), the fused store (second) and the fallback kernel (third)."""
+    a, b = _u((n, k), 7), _u((k, m), 8)
+    bias, res = _u((m,), 9), _u((n, m), 10)
+    exact = oracle.matmul(a, b, threads=True).astype(np.float64)
+    bound = G.gemm_error_bound(a, b)
+    got = G.gemm_ex(_stored(a, True), b, True, False, bias=bias, residual=res)
+    ref = exact + bias + res
+    assert (np.abs(got - ref) <= bound + 1e-6 * (1 + np.abs(ref))).all()
+    y, pre = G.gemm_ex(a, _stored(b, True), False, True, bias=bias, act=1)
+    assert (np.abs(pre - (exact + bias)) <= bound + 1e-6 * (1 + np.abs(exact))).all()
+    np.testing.assert_allclose(y, oracle.gelu_fwd(pre), rtol=1e-5, atol=1e-6)
