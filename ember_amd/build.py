@@ -40,6 +40,7 @@ HIP_SOURCES = [
     ("optim.hip", []),
     ("layernorm.hip", []),
     ("block_ops.hip", []),
+    ("softmax.hip", []),
 ]
 
 HIP_FLAGS = [

@@ -12,8 +12,12 @@
 //    coalesced (operators_gpu.cu:138-151 stores with a stride of n);
 //  * sum() reduces on the device in double and copies one float back,
 //    instead of copying the whole tensor to the host (operators_gpu.cu:153-166).
-// sum_axis / max_axis keep one thread per output walking the axis in index
-// order with a float accumulator, the exact arithmetic of the reference.
+// sum_axis / max_axis keep the reference's arithmetic exactly: each output is
+// folded along the axis in index order with a float accumulator (sum from
+// 0.0f, max from the first element with fmaxf).  Where the axis is the last
+// one (inner == 1) the reference's one-thread-per-output loads are strided by
+// the row length; here a wave owns 64 rows and stages 64-column chunks
+// through LDS with row-contiguous loads before each lane folds its row.
 #include <math.h>
 
 #include "common.h"
@@ -210,6 +214,34 @@ __global__ void k_max_axis(const float *a, float *out, int outer, int inner, int
     }
 }
 
+// Last-axis reduction of up to 64 rows per wave (see the file comment).
+template <bool MAX>
+__global__ __launch_bounds__(64) void k_reduce_rows(const float *a, float *out, int rows, int L)
+{
+    __shared__ float tile[64 * 65];
+    const int lane = threadIdx.x;
+    const int r0 = blockIdx.x * 64;
+    const int nr = min(64, rows - r0);
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < L; c0 += 64) {
+        const int c = c0 + lane;
+        if (c < L) {
+#pragma unroll 16
+            for (int r = 0; r < nr; ++r) tile[r * 65 + lane] = a[(int64_t)(r0 + r) * L + c];
+        }
+        __syncthreads();
+        if (lane < nr) {
+            const int nc = min(64, L - c0);
+            const float *t = tile + lane * 65;
+            int j = 0;
+            if (MAX && c0 == 0) acc = t[j++];
+            for (; j < nc; ++j) acc = MAX ? fmaxf(acc, t[j]) : acc + t[j];
+        }
+        __syncthreads();
+    }
+    if (lane < nr) out[r0 + lane] = acc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -249,6 +281,12 @@ void sum_axis(const float *a, float *out, int outer_stride, int inner_stride, in
 {
     const int total = outer_stride * inner_stride;
     if (total <= 0) return;
+    if (inner_stride == 1 && axis_dim > 1) {
+        hipLaunchKernelGGL(k_reduce_rows<false>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
+                           out, outer_stride, axis_dim);
+        ember::launch_ok("sum_axis");
+        return;
+    }
     hipLaunchKernelGGL(k_sum_axis, dim3(grid_for(total)), dim3(kBlock), 0, 0, a, out, outer_stride,
                        inner_stride, axis_dim);
     ember::launch_ok("sum_axis");
@@ -258,6 +296,12 @@ void max_axis(const float *a, float *out, int outer_stride, int inner_stride, in
 {
     const int total = outer_stride * inner_stride;
     if (total <= 0 || axis_dim <= 0) return;
+    if (inner_stride == 1 && axis_dim > 1) {
+        hipLaunchKernelGGL(k_reduce_rows<true>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
+                           out, outer_stride, axis_dim);
+        ember::launch_ok("max_axis");
+        return;
+    }
     hipLaunchKernelGGL(k_max_axis, dim3(grid_for(total)), dim3(kBlock), 0, 0, a, out, outer_stride,
                        inner_stride, axis_dim);
     ember::launch_ok("max_axis");

@@ -537,6 +537,39 @@ static PyObject *py_max_axis(PyObject *m, PyObject *args)
     return do_axis(args, max_axis, "_max_axis");
 }
 
+/* _softmax(a, shape, axis) -> softmax along axis in one launch (same shape);
+ * replaces the five-operator composition of ember/tensor/tensor.py:430-437. */
+static PyObject *py_softmax(PyObject *module, PyObject *args)
+{
+    TensorObject *a;
+    PyObject *shape_t;
+    int axis;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!i", &TensorType, &a, &PyTuple_Type, &shape_t, &axis)) return NULL;
+    int shape[16], nd;
+    if (int_tuple(shape_t, shape, &nd)) return NULL;
+    if (axis < 0 || axis >= nd) {
+        PyErr_Format(PyExc_ValueError, "Axis %d out of bound for %d dim Tensor", axis, nd);
+        return NULL;
+    }
+    Py_ssize_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= shape[i];
+    for (int i = axis + 1; i < nd; i++) inner *= shape[i];
+    if (outer * inner * shape[axis] != a->size) {
+        PyErr_SetString(PyExc_ValueError, "Shape does not match the Tensor's size");
+        return NULL;
+    }
+    if (!fits_int(a->size, "_softmax")) return NULL;
+    TensorObject *r = alloc_tensor(a->size);
+    if (!r) return NULL;
+    int st = softmax_axis(a->d_ptr, r->d_ptr, (int)outer, (int)inner, shape[axis]);
+    if (raise_status(st, "_softmax")) {
+        Py_DECREF(r);
+        return NULL;
+    }
+    return (PyObject *)r;
+}
+
 /* ---- attention (new; no reference counterpart) ---- */
 
 static int check_bhsd(TensorObject *t, long long B, long long H, long long S, long long D,
@@ -966,6 +999,7 @@ static PyMethodDef module_methods[] = {
     METHOD("_sum", py_sum, "sum of all elements"),
     METHOD("_sum_axis", py_sum_axis, "sum over one axis"),
     METHOD("_max_axis", py_max_axis, "max over one axis"),
+    METHOD("_softmax", py_softmax, "softmax along one axis, one launch"),
     METHOD("_attention_fwd", py_attention_fwd, "fused attention forward -> (o, lse)"),
     METHOD("_attention_bwd", py_attention_bwd, "fused attention backward -> (dq, dk, dv)"),
     METHOD("_adam_step", py_adam_step, "fused Adam step over lists of _Tensor, in place"),

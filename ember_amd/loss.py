@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import math
 
-from ember_amd.tensor import Tensor, sum as _sum
+from ember_amd.tensor import Tensor, amax, exp, log, sum as _sum
 
 
 class MSELoss:
@@ -29,4 +29,32 @@ class MSELoss:
         return (2.0 / self.n) * self.diff
 
 
-__all__ = ["MSELoss"]
+class CrossEntropyLoss:
+    """Softmax cross-entropy over (batch, classes) logits against one-hot (or
+    probability) targets, averaged over the batch (``losses.py:29-56``):
+    forward -sum(target * log_softmax(pred)) / batch with the log-sum-exp
+    shift; backward (softmax(pred) - target) / batch."""
+
+    def __init__(self) -> None:
+        self.probs: Tensor | None = None
+        self.target: Tensor | None = None
+        self.n = 0
+
+    def forward(self, pred: Tensor, target: Tensor) -> float:
+        self.n = pred.shape[0]
+        self.target = target
+        shifted = pred - amax(pred, axis=-1, keepdims=True)
+        log_probs = shifted - log(_sum(exp(shifted), axis=-1, keepdims=True))
+        self.probs = exp(log_probs)
+        return -_sum(target * log_probs) / self.n
+
+    def __call__(self, pred: Tensor, target: Tensor) -> float:
+        return self.forward(pred, target)
+
+    def backward(self) -> Tensor:
+        if self.probs is None or self.target is None:
+            raise RuntimeError("forward() must run before backward()")
+        return (self.probs - self.target) / self.n
+
+
+__all__ = ["MSELoss", "CrossEntropyLoss"]

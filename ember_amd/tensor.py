@@ -358,11 +358,11 @@ def amax(a: Tensor, axis: int, keepdims: bool = False) -> Tensor:
 
 
 def softmax(a: Tensor, axis: int = -1) -> Tensor:
-    """Softmax along ``axis``: shift by the max, exp, divide by the sum."""
+    """Softmax along ``axis``: shift by the max, exp, divide by the sum
+    (``tensor.py:430-437``), fused into one device launch."""
     _need_tensor(a, "softmax()")
     ax = _axis(a, axis)
-    e = exp(a - amax(a, axis=ax, keepdims=True))
-    return e / sum(e, axis=ax, keepdims=True)
+    return Tensor._from_core(C._softmax(a._core, a.shape, ax), a.shape)
 
 
 # ---------------------------------------------------------------- attention

@@ -93,6 +93,12 @@ int sum_axis_product(const int *shape, int start, int end);
  * max in index order per output, as operators_gpu.cu:175-219. */
 void sum_axis(const float *a, float *out, int outer_stride, int inner_stride, int axis_dim);
 void max_axis(const float *a, float *out, int outer_stride, int inner_stride, int axis_dim);
+/* out = exp(a - max) / sum(exp(a - max)) along the middle axis of
+ * (outer, axis_dim, inner), in one launch: Ember's softmax
+ * (ember/tensor/tensor.py:430-437, five operators in the reference) with the
+ * same per-element fp32 operations; along the last axis (inner == 1) the sum
+ * is taken in a fixed tree order instead of index order.  Returns a status. */
+int softmax_axis(const float *a, float *out, int outer, int inner, int axis_dim);
 
 /* ---- fused attention (new; no reference counterpart exists) ----
  *

@@ -190,6 +190,47 @@ def _ref_softmax_rows(R, x: np.ndarray) -> np.ndarray:
     return out
 
 
+def _as3(x: np.ndarray, axis: int):
+    """(outer, L, inner) view of a C-contiguous float32 array around `axis`."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    outer = int(np.prod(x.shape[:axis], dtype=np.int64))
+    inner = int(np.prod(x.shape[axis + 1:], dtype=np.int64))
+    return x.reshape(outer, x.shape[axis], inner), outer, inner
+
+
+def ref_axis_reduce(x: np.ndarray, axis: int, kind: str) -> np.ndarray:
+    """The reference's sum_axis / max_axis (operators_cpu.c:92-120) over
+    `axis` (keepdims shape)."""
+    R = ref_lib()
+    x3, outer, inner = _as3(x, axis)
+    out = np.empty((outer, 1, inner), dtype=np.float32)
+    getattr(R, kind + "_axis")(x3, out, outer, inner, x3.shape[1])
+    shape = list(x.shape)
+    shape[axis] = 1
+    return out.reshape(shape)
+
+
+def ref_softmax(x: np.ndarray, axis: int) -> np.ndarray:
+    """em.softmax(x, axis) through the reference's own CPU operators:
+    max_axis -> sub_broadcasted -> exponent_tensor -> sum_axis ->
+    truediv_broadcasted (ember/tensor/tensor.py:430-437)."""
+    R = ref_lib()
+    x3, outer, inner = _as3(x, axis)
+    L = x3.shape[1]
+    mx = np.empty((outer, 1, inner), dtype=np.float32)
+    R.max_axis(x3, mx, outer, inner, L)
+    shp, sa, sb = _bcast(x3.shape, mx.shape)
+    shifted = np.empty_like(x3)
+    R.sub_broadcasted(x3, mx, shifted, shp, sa, sb, 3)
+    e = np.empty_like(x3)
+    R.exponent_tensor(shifted, e, x3.size)
+    s = np.empty((outer, 1, inner), dtype=np.float32)
+    R.sum_axis(e, s, outer, inner, L)
+    out = np.empty_like(x3)
+    R.truediv_broadcasted(e, s, out, shp, sa, sb, 3)
+    return out.reshape(x.shape)
+
+
 def _ref_mm(R, a, b):
     n, k = a.shape
     m = b.shape[1]

@@ -404,3 +404,28 @@ def test_decoder_oracle_causal_rows_see_only_the_past():
     x2[3:] += 1.0
     y2, _ = decoder.forward(params, x2, B, S, H, True)
     np.testing.assert_array_equal(y[:3], y2[:3])
+
+
+# ---- axis reductions and softmax through the reference's CPU operators ----
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("shape,axis", [((7, 33), 1), ((7, 33), 0), ((3, 5, 9), 1), ((1, 1000), 1)])
+def test_ref_axis_reduce_is_a_sequential_float_fold(shape, axis):
+    """sum_axis is a float32 fold in index order: it equals the last entry of
+    a float32 running sum (np.add.accumulate is strictly sequential), and
+    max_axis equals np.max exactly."""
+    x = np.random.default_rng(5).standard_normal(shape).astype(np.float32) * 100
+    run = np.add.accumulate(x, axis=axis, dtype=np.float32)
+    last = np.take(run, [-1], axis=axis)
+    np.testing.assert_array_equal(oracle.ref_axis_reduce(x, axis, "sum"), last)
+    np.testing.assert_array_equal(oracle.ref_axis_reduce(x, axis, "max"), x.max(axis=axis, keepdims=True))
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("shape,axis", [((5, 40), 1), ((5, 40), 0), ((3, 4, 6), 1)])
+def test_ref_softmax_against_float64(shape, axis):
+    x = np.random.default_rng(6).standard_normal(shape).astype(np.float32) * 4
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=axis, keepdims=True))
+    np.testing.assert_allclose(oracle.ref_softmax(x, axis), e / e.sum(axis=axis, keepdims=True),
+                               rtol=2e-6, atol=1e-9)
