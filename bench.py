@@ -228,6 +228,42 @@ def secondary(L, ev):
                                  "frac_of_hbm_peak": round(28.0 * nparam / ms / 1e6 / PEAK_HBM_GBS, 4)}
     del tens
 
+    # Softmax over rows (an (8192, 1024) score block) fused in one launch,
+    # against Ember's five-operator composition on the same device, and the
+    # row sums that keep the reference's sequential order.
+    rows, cols = 8192, 1024
+    x = DeviceArray((rows * cols,), rng.standard_normal(rows * cols).astype(np.float32))
+    y = DeviceArray((rows * cols,))
+    r = DeviceArray((rows,))
+    ms = _timed(ev, lambda: L.softmax_axis(x.ptr, y.ptr, rows, 1, cols), 20)
+    from ember_amd import Tensor, softmax as em_softmax, amax as em_amax, exp as em_exp, sum as em_sum
+    xt = Tensor(np.random.default_rng(1).standard_normal((rows, cols), dtype=np.float32))
+
+    def composed():
+        e = em_exp(xt - em_amax(xt, axis=1, keepdims=True))
+        return e / em_sum(e, axis=1, keepdims=True)
+
+    composed()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        composed()
+    L.sync_device()
+    comp_ms = (time.perf_counter() - t0) * 1e3 / 5
+    em_softmax(xt)
+    L.sync_device()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        em_softmax(xt)
+    L.sync_device()
+    fused_py_ms = (time.perf_counter() - t0) * 1e3 / 5
+    sum_ms = _timed(ev, lambda: L.sum_axis(x.ptr, r.ptr, rows, 1, cols), 20)
+    out["softmax_rows_8192x1024"] = {
+        "fused_kernel_ms": round(ms, 4), "hbm_gbs": round(8.0 * rows * cols / ms / 1e6, 1),
+        "fused_python_ms": round(fused_py_ms, 4), "composed_five_ops_python_ms": round(comp_ms, 4),
+        "sum_axis_ms": round(sum_ms, 4), "sum_axis_hbm_gbs": round(4.0 * rows * cols / sum_ms / 1e6, 1)}
+    capi.check(what="softmax")
+    del x, y, r, xt
+
     # Config 5: one decoder-block training step (forward, MSE loss, backward,
     # fused Adam) at d=1024, 16 heads of 64, S=1024, B=8, causal, through the
     # Python front-end.  Wall-clock per step (the loss is read back each step,
@@ -265,12 +301,19 @@ def main(argv=None):
                     help="after the timed steps, run one plain copy-like kernel "
                          "(negate_tensor: reads and writes N MiB) so rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against known bytes")
+    ap.add_argument("--decoder-steps", type=int, default=0,
+                    help="only run config 5's decoder-block training step this many "
+                         "times and print its record (for profiling)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on exactly one GPU (no multi-GPU path); "
               "use --gpus 1", file=sys.stderr)
         return 2
+    if args.decoder_steps > 0:
+        print(json.dumps({"config5_decoder_step": decoder_step(8, 1024, 1024, 16, args.decoder_steps)}),
+              flush=True)
+        return 0
 
     B, H, S, D = args.batch, args.heads, args.seq, args.head_dim
     causal = not args.non_causal
