@@ -24,6 +24,12 @@
 //     dS of all 4 waves goes through LDS so that dQ(32 x D) = dS . K over the
 //     workgroup's 128 keys is one more MFMA product per wave, added to the
 //     global dQ with hardware fp32 atomics (dq must be device memory).
+//     That product is software-pipelined by one block: block j's step runs
+//     the dQ MFMAs of block j-1 in between block j's softmax instructions,
+//     so the matrix core keeps working while the softmax's VALU and
+//     transcendental instructions issue (one wave per SIMD: no other wave
+//     could fill the gap), and the step ends with one pair of barriers
+//     around the dS exchange instead of two separated phases.
 //
 // Pipelining and instruction economy.  The next query block's Q, dO, lse2
 // and delta are copied HBM -> LDS directly (gfx950 global_load_lds_dwordx4,
@@ -32,12 +38,15 @@
 // K: rows of D with the second half of the keys shifted by 32 floats) rather
 // than XOR swizzles, chosen so that every LDS access in the loop is a per-lane
 // base register plus a compile-time offset: the loop then spends its VALU
-// issue slots on the softmax and not on address arithmetic.  Blocks that
-// cross the causal diagonal or the last key hold the mask; all others run a
-// mask-free path.
+// issue slots on the softmax and not on address arithmetic.  The causal and
+// key-tail mask is an integer compare per element against a per-lane
+// threshold (no branches inside a step); workgroups with neither run a
+// mask-free copy of the loop.
 #pragma once
 
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.h"
 #include "lds_dma.h"
@@ -172,12 +181,104 @@ __device__ __forceinline__ void bwd_fetch(const BwdBlock &k, int m0, float *__re
     }
 }
 
-// One query block: phase 1 on (qs, gs, st), barrier, dS to LDS, barrier,
-// phase 2 (dQ); meanwhile the next block is copied into (qn, gn, stn).  The
-// buffers are distinct __restrict__ pointers so that the compiler can tell
-// the LDS-bound copies from the reads of the current buffers and does not
-// wait for them before every LDS read.
-template <int D, bool CAUSAL>
+// dQ of one query block: dQ[m0:m0+32, 32*dblk:+32] += scale * dS . K over
+// this wave's share of the workgroup's keys, dS read from LDS.  The dQ
+// product of the previous block is issued in the middle of the next block's
+// step, interleaved with that block's softmax (see bwd_step).
+template <int D>
+struct DqState {
+    int sa, kbase;
+};
+
+template <int D>
+__device__ __forceinline__ DqState<D> dq_state(int w)
+{
+    typedef BwdLayout<D> L;
+    constexpr int DB = L::DB;
+    const int lane = threadIdx.x & 63;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    const int dblk = w % DB;
+    const int nbase = (w / DB) * L::NK;
+    DqState<D> st;
+    st.sa = l32 * L::SSTR + nbase + h32 * L::NKH;
+    st.kbase = (nbase + h32 * L::NKH) * D + (nbase / L::NKH + h32) * 32 + 32 * dblk + l32;
+    return st;
+}
+
+// Adds the finished dQ block (rows m0..m0+31) to global memory.
+template <int D>
+__device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, int m0, const f32x16 &qacc)
+{
+    constexpr int DB = BwdLayout<D>::DB;
+    const int lane = threadIdx.x & 63;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    const int dblk = k.w % DB;
+    // Row i of the block: wave-uniform row base + unsigned lane offset.
+    float *dqb = k.dqp + (int64_t)m0 * k.in_ss + 32 * dblk;
+    const unsigned qoff = (unsigned)(4 * h32 * k.in_ss + l32);
+    if (m0 + kBq <= k.S) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
+            unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
+            if (m0 + acc_row(i, h32) < k.S) unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
+        }
+    }
+}
+
+// The dQ product of the previous block (when PREV) fused with this block's
+// softmax: P = exp2(S*c - lse2), masked where t > 8(i/4) + i%4 (when MASK),
+// dS = P * (dP - delta).  sacc / pacc hold S / dP on entry, P / dS on exit.
+template <int D, bool PREV, bool MASK>
+__device__ __forceinline__ void dq_softmax(const BwdArgs &a, const float *__restrict__ ds,
+                                           const float *__restrict__ kall, const DqState<D> &dqs,
+                                           const f32x4 (&l2v)[4], const f32x4 (&dlv)[4], int t,
+                                           f32x16 &sacc, f32x16 &pacc, f32x16 &qacc)
+{
+    typedef BwdLayout<D> L;
+    constexpr int NIT = L::NKH / 4;  // dQ k-steps of 4 MFMAs
+    constexpr int EPI = 16 / NIT;    // softmax elements per k-step
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        if (PREV) {
+            const f32x4 sf = *(const f32x4 *)&ds[dqs.sa + 4 * it];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                qacc = mfma_32x32x2(sf[j], kall[dqs.kbase + (4 * it + j) * D], qacc);
+        }
+#pragma unroll
+        for (int e = 0; e < EPI; ++e) {
+            const int i = it * EPI + e;
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2v[i >> 2][i & 3]));
+            if (MASK) p = t > 8 * (i >> 2) + (i & 3) ? 0.0f : p;
+            sacc[i] = p;                                   // P[m][n]
+            pacc[i] = p * (pacc[i] - dlv[i >> 2][i & 3]);  // dS[m][n]
+        }
+    }
+}
+
+// One query block qb, software-pipelined with the previous one:
+//   1. copy block qb+1 into (qn, gn, stn);
+//   2. S = Q K^T and dP = dO V^T of block qb (MFMA);
+//   3. the dQ product of block qb-1 (dS in LDS since the last barrier),
+//      interleaved with the softmax of block qb: its VALU work issues while
+//      the dQ MFMAs run, instead of leaving the matrix core idle;
+//   4. dQ of block qb-1 to global memory (atomics);
+//   5. dV += P^T dO, dK += dS^T Q of block qb;
+//   6. barrier (every wave has read dS of block qb-1), dS of block qb to
+//      LDS, wait for the copies, barrier.
+// The mask is applied branch-free (an integer compare per element against a
+// per-lane threshold), so steps 2 and 3 are one basic block.  Keys a wave
+// cannot see in this block (causal, above the diagonal) get P = 0 by the same
+// compare, so no wave skips the block.
+template <int D, bool CAUSAL, bool PREV, bool MASK>
 __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, int qb,
                                          const float *__restrict__ qs,
                                          const float *__restrict__ gs,
@@ -185,7 +286,8 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
                                          float *__restrict__ qn, float *__restrict__ gn,
                                          float *__restrict__ stn,
                                          const float *__restrict__ kall, const float *kr,
-                                         const float *vr, f32x16 *dvacc, f32x16 *dkacc)
+                                         const float *vr, f32x16 *dvacc, f32x16 *dkacc,
+                                         int tail_bias)
 {
     typedef BwdLayout<D> L;
     constexpr int DH = D / 2;
@@ -193,18 +295,13 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
     const int lane = threadIdx.x & 63;
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
-    const int w = k.w;
     const int m0 = qb * kBq;
-    const int S = k.S;
 
     if (qb + 1 < k.nq) bwd_fetch<D>(k, m0 + kBq, qn, gn, stn);
 
-    // ---- phase 1: S, dP, P, dS; dV += P^T dO, dK += dS^T Q ----
-    f32x16 pacc;
-    const bool active = !CAUSAL || k.n0w <= m0 + kBq - 1;
-    if (active) {
-        f32x16 sacc = zero16();
-        pacc = zero16();
+    // ---- S, dP ----
+    f32x16 sacc = zero16(), pacc = zero16();
+    {
         const int abase = l32 * L::QSTR + h32 * DH;
 #pragma unroll
         for (int kk = 0; kk < DH; kk += 4) {
@@ -216,85 +313,67 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
                 pacc = mfma_32x32x2(gf[j], vr[kk + j], pacc);
             }
         }
-        // Row statistics of rows acc_row(4g + 0..3, h32) = 8g + 4*h32 + 0..3.
-        f32x4 l2v[4], dlv[4];
+    }
+    // Row statistics of rows acc_row(4g + 0..3, h32) = 8g + 4*h32 + 0..3.
+    f32x4 l2v[4], dlv[4];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            l2v[g] = *(const f32x4 *)&st[8 * g + 4 * h32];
-            dlv[g] = *(const f32x4 *)&st[kBq + 8 * g + 4 * h32];
-        }
-        const bool need_mask = k.key_tail || (CAUSAL && k.n0w + kBkw - 1 > m0);
-        if (!need_mask) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2v[i >> 2][i & 3]));
-                sacc[i] = p;                                   // P[m][n]
-                pacc[i] = p * (pacc[i] - dlv[i >> 2][i & 3]);  // dS[m][n]
-            }
-        } else {
-            const int nl = k.n0w + l32;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int r = acc_row(i, h32);
-                float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2v[i >> 2][i & 3]));
-                if (nl >= S || (CAUSAL && nl > m0 + r)) p = 0.0f;
-                sacc[i] = p;
-                pacc[i] = p * (pacc[i] - dlv[i >> 2][i & 3]);
-            }
-        }
+    for (int g = 0; g < 4; ++g) {
+        l2v[g] = *(const f32x4 *)&st[8 * g + 4 * h32];
+        dlv[g] = *(const f32x4 *)&st[kBq + 8 * g + 4 * h32];
+    }
+    // ---- dQ of the previous block, interleaved with this block's softmax ----
+    // Blocks that cross the diagonal or the last key take the masked copy of
+    // the loop; each copy is one basic block.
+    f32x16 qacc = zero16();
+    const DqState<D> dqs = dq_state<D>(k.w);
+    // P[m][n] = 0 where t > 8(i/4) + i%4 (see the mask note above).
+    const int t = (CAUSAL ? k.n0w + l32 - m0 - 4 * h32 : -1) + tail_bias;
+    dq_softmax<D, PREV, MASK>(a, ds, kall, dqs, l2v, dlv, t, sacc, pacc, qacc);
+    if (PREV) dq_store<D>(a, k, m0 - kBq, qacc);
+
+    // ---- dV += P^T dO, dK += dS^T Q ----
+    {
+        typedef typename VecN<DB>::T OpT;
         const int bbase = 4 * h32 * L::QSTR + DB * l32;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int off = bbase + ((i >> 2) * 8 + (i & 3)) * L::QSTR;
-            const typename VecN<DB>::T gf = *(const typename VecN<DB>::T *)&gs[off];
-            const typename VecN<DB>::T qf = *(const typename VecN<DB>::T *)&qs[off];
+            const OpT gf = *(const OpT *)&gs[off];
+            const OpT qf = *(const OpT *)&qs[off];
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 dvacc[db] = mfma_32x32x2(sacc[i], vget<DB>(gf, db), dvacc[db]);
                 dkacc[db] = mfma_32x32x2(pacc[i], vget<DB>(qf, db), dkacc[db]);
             }
         }
-    } else {
-        pacc = zero16();  // no visible key: this wave's dS block is 0
     }
-    // Every wave has finished the previous block's phase 2 (its reads of ds).
+    // Every wave has read the previous block's dS.
     __syncthreads();
     {
-        const int sbase = 4 * h32 * L::SSTR + kBkw * w + l32;
+        const int sbase = 4 * h32 * L::SSTR + kBkw * k.w + l32;
 #pragma unroll
         for (int i = 0; i < 16; ++i) ds[sbase + ((i >> 2) * 8 + (i & 3)) * L::SSTR] = pacc[i];
     }
     wait_vmem();  // this wave's copies into (qn, gn, stn) have landed
     __syncthreads();
+}
 
-    // ---- phase 2: dQ[m0:m0+32, 32*dblk:+32] += scale * dS . K (this wave's keys) ----
-    const int dblk = w % DB;
-    const int nbase = (w / DB) * L::NK;
+// dQ of the last block (its dS is in LDS after the last step's barrier).
+template <int D>
+__device__ __forceinline__ void bwd_last_dq(const BwdArgs &a, const BwdBlock &k, int m0,
+                                            const float *__restrict__ ds,
+                                            const float *__restrict__ kall)
+{
+    typedef BwdLayout<D> L;
+    const DqState<D> dqs = dq_state<D>(k.w);
     f32x16 qacc = zero16();
-    const int sa = l32 * L::SSTR + nbase + h32 * L::NKH;
-    const int kbase = (nbase + h32 * L::NKH) * D + (nbase / L::NKH + h32) * 32 + 32 * dblk + l32;
 #pragma unroll
     for (int kk = 0; kk < L::NKH; kk += 4) {
-        const f32x4 sf = *(const f32x4 *)&ds[sa + kk];
+        const f32x4 sf = *(const f32x4 *)&ds[dqs.sa + kk];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) qacc = mfma_32x32x2(sf[j], kall[kbase + (kk + j) * D], qacc);
+        for (int j = 0; j < 4; ++j) qacc = mfma_32x32x2(sf[j], kall[dqs.kbase + (kk + j) * D], qacc);
     }
-    // Row i of the block: wave-uniform row base + unsigned lane offset.
-    float *dqb = k.dqp + (int64_t)m0 * k.in_ss + 32 * dblk;
-    const unsigned qoff = (unsigned)(4 * h32 * k.in_ss + l32);
-    if (m0 + kBq <= S) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
-            unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
-            if (m0 + acc_row(i, h32) < S) unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
-        }
-    }
+    dq_store<D>(a, k, m0, qacc);
 }
 
 template <int D, bool CAUSAL>
@@ -394,13 +473,26 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     wait_vmem();
     __syncthreads();
 
-    for (int qb = qstart; qb < k.nq; qb += 2) {
-        bwd_step<D, CAUSAL>(a, k, qb, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1, Kall, kr, vr, dvacc,
-                            dkacc);
-        if (qb + 1 < k.nq)
-            bwd_step<D, CAUSAL>(a, k, qb + 1, Qs1, dOs1, St1, dSs, Qs0, dOs0, St0, Kall, kr, vr,
-                                dvacc, dkacc);
-    }
+    // Keys past the sequence end: P = 0 whatever the row (see bwd_step).
+    // Without a causal mask or such keys no block needs the mask.
+    const int tail_bias = k.n0w + l32 >= S ? (1 << 24) : 0;
+    auto walk = [&](auto mask) {
+        constexpr bool M = decltype(mask)::value;
+        bwd_step<D, CAUSAL, false, M>(a, k, qstart, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1, Kall, kr,
+                                      vr, dvacc, dkacc, tail_bias);
+        for (int qb = qstart + 1; qb < k.nq; qb += 2) {
+            bwd_step<D, CAUSAL, true, M>(a, k, qb, Qs1, dOs1, St1, dSs, Qs0, dOs0, St0, Kall, kr,
+                                         vr, dvacc, dkacc, tail_bias);
+            if (qb + 1 < k.nq)
+                bwd_step<D, CAUSAL, true, M>(a, k, qb + 1, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1,
+                                             Kall, kr, vr, dvacc, dkacc, tail_bias);
+        }
+    };
+    if (CAUSAL || k.key_tail)
+        walk(std::true_type{});
+    else
+        walk(std::false_type{});
+    bwd_last_dq<D>(a, k, (k.nq - 1) * kBq, dSs, Kall);
 
     // dK (scaled) and dV rows of this wave's keys: register i -> key
     // n0w + acc_row(i, h32), lane -> d = DB*l32 + db.
