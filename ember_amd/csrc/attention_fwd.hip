@@ -8,6 +8,9 @@
 // each wave owns 32 queries for the whole kernel.  The workgroup walks the
 // keys in tiles of 64: every tile of K and V is read from HBM once with
 // coalesced 128-bit loads and staged in LDS, where the 4 waves share it.
+// Short sequences pack heads instead: S <= 32 puts 4 heads in a workgroup
+// (one per wave, tiles of 32 keys) and S <= 64 puts 2 (two waves each), so
+// that no wave idles and the HBM-bound forward keeps every wave loading.
 //
 // Per tile and wave (all products on v_mfma_f32_32x32x2f32):
 //   S^T (64 keys x 32 queries) = K_tile . Q^T   -- K from LDS, Q^T resident in
@@ -32,27 +35,30 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBr = 32 * kWaves;  // queries per workgroup
-constexpr int kBc = 64;           // keys per tile
+constexpr int kBr = 32 * kWaves;  // queries per workgroup (one head per workgroup)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 struct FwdArgs {
     const float *q, *k, *v;
     float *o, *lse;
-    int H, S, nqb;
+    int H, S, nqb, nbh;
     float c;  // scale * log2(e)
     int64_t in_sb, in_sh, in_ss, out_sb, out_sh, out_ss;
 };
 
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
+// HP heads per workgroup (1, 2 or 4), each with 4/HP waves of 32 queries,
+// and key tiles of BC (64, or 32 when HP = 4).
+template <int D, bool CAUSAL, int HP, int BC>
+__global__ __launch_bounds__(kThreads, HP == 1 ? 2 : 1) void attn_fwd_kernel(FwdArgs a)
 {
     constexpr int DH = D / 2;   // contraction length per lane half (k-steps)
     constexpr int DB = D / 32;  // 32-row blocks of O^T
     constexpr int KSTR = D + 4; // padded K row: conflict-free column reads
-    __shared__ float Ks[kBc * KSTR];
-    __shared__ float Vs[kBc * D];
+    constexpr int QB = kWaves / HP;  // waves (32-query blocks) per head
+    constexpr int kBc = BC;
+    __shared__ float Ks[HP * kBc * KSTR];
+    __shared__ float Vs[HP * kBc * D];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -61,16 +67,30 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
     const int l32 = lane & 31;
 
     // Heavy (late) query blocks first so the causal triangle load-balances.
-    const int BH = (int)(gridDim.x / a.nqb);
-    const int qbr = blockIdx.x / BH;
-    const int bh = blockIdx.x - qbr * BH;
-    const int qb = CAUSAL ? (a.nqb - 1 - qbr) : qbr;
+    int bh, qb, bh0;
+    if (HP == 1) {
+        const int BH = (int)(gridDim.x / a.nqb);
+        const int qbr = blockIdx.x / BH;
+        bh = blockIdx.x - qbr * BH;
+        qb = CAUSAL ? (a.nqb - 1 - qbr) : qbr;
+        bh0 = bh;
+    } else {
+        bh0 = blockIdx.x * HP;
+        bh = bh0 + w / QB;
+        qb = 0;
+    }
+    // A wave past the last head computes on the last head's data and stores
+    // nothing (it still takes part in every barrier).
+    const bool head_ok = bh < a.nbh;
+    if (!head_ok) bh = a.nbh - 1;
     const int b = bh / a.H;
     const int hh = bh - b * a.H;
     const int S = a.S;
-    const int q0 = qb * kBr;
-    const int m0 = q0 + 32 * w;
+    const int q0 = qb * 32 * QB;
+    const int m0 = q0 + 32 * (w % QB);
     const int mq = m0 + l32;
+    const float *__restrict__ kslab = Ks + (HP == 1 ? 0 : (w / QB) * kBc * KSTR);
+    const float *__restrict__ vslab = Vs + (HP == 1 ? 0 : (w / QB) * kBc * D);
 
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const float *__restrict__ qp = a.q + in_base;
@@ -94,11 +114,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
     float mrun = -INFINITY;  // reference max of s*c for query mq (see below)
     float lrun = 0.0f;       // this lane half's share of the running sum
 
-    const int kend = CAUSAL ? min(S, q0 + kBr) : S;
+    const int kend = CAUSAL ? min(S, q0 + 32 * QB) : S;
     const int ntiles = (kend + kBc - 1) / kBc;
-    constexpr int kLoads = kBc * D / 4 / kThreads;
-    const float *__restrict__ kp = a.k + in_base;
-    const float *__restrict__ vp = a.v + in_base;
+    constexpr int kLoads = HP * kBc * D / 4 / kThreads;
+    constexpr int kRowsPerLoad = kThreads / (D / 4);
+    static_assert(HP == 1 || kBc % kRowsPerLoad == 0, "a load row block must lie in one head");
+    // Base of the head each tile row block belongs to (HP > 1: head bh0 + hp,
+    // clamped to the last head).
+    auto head_base = [&](int hp) -> int64_t {
+        if (HP == 1) return in_base;
+        int h = bh0 + hp;
+        if (h >= a.nbh) h = a.nbh - 1;
+        const int hb = h / a.H;
+        return (int64_t)hb * a.in_sb + (int64_t)(h - hb * a.H) * a.in_sh;
+    };
 
     for (int t = 0; t < ntiles; ++t) {
         // Per-lane offsets below derive from `tid`, which the empty asm makes
@@ -107,30 +136,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
         int tid = threadIdx.x;
         asm volatile("" : "+v"(tid));
         const int n0 = t * kBc;
-        const float *kt = kp + (int64_t)n0 * a.in_ss;
-        const float *vt = vp + (int64_t)n0 * a.in_ss;
         __syncthreads();
         if (n0 + kBc <= S) {
 #pragma unroll
             for (int it = 0; it < kLoads; ++it) {
+                const int hp = it * kRowsPerLoad / kBc;  // compile-time
+                const int64_t hbase = head_base(hp) + (int64_t)n0 * a.in_ss;
                 const int idx = it * kThreads + tid;
                 const int r = idx / (D / 4);
                 const int c4 = idx - r * (D / 4);
-                const unsigned off = (unsigned)(r * (int)a.in_ss + 4 * c4);
-                *(f32x4 *)&Ks[r * KSTR + 4 * c4] = *(const f32x4 *)(kt + off);
-                *(f32x4 *)&Vs[r * D + 4 * c4] = *(const f32x4 *)(vt + off);
+                const int rr = r - hp * kBc;
+                const unsigned off = (unsigned)(rr * (int)a.in_ss + 4 * c4);
+                *(f32x4 *)&Ks[r * KSTR + 4 * c4] = *(const f32x4 *)(a.k + hbase + off);
+                *(f32x4 *)&Vs[r * D + 4 * c4] = *(const f32x4 *)(a.v + hbase + off);
             }
         } else {
 #pragma unroll
             for (int it = 0; it < kLoads; ++it) {
+                const int hp = it * kRowsPerLoad / kBc;
+                const int64_t hbase = head_base(hp) + (int64_t)n0 * a.in_ss;
                 const int idx = it * kThreads + tid;
                 const int r = idx / (D / 4);
                 const int c4 = idx - r * (D / 4);
+                const int rr = r - hp * kBc;
                 f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-                if (n0 + r < S) {
-                    const unsigned off = (unsigned)(r * (int)a.in_ss + 4 * c4);
-                    kv = *(const f32x4 *)(kt + off);
-                    vv = *(const f32x4 *)(vt + off);
+                if (n0 + rr < S) {
+                    const unsigned off = (unsigned)(rr * (int)a.in_ss + 4 * c4);
+                    kv = *(const f32x4 *)(a.k + hbase + off);
+                    vv = *(const f32x4 *)(a.v + hbase + off);
                 }
                 *(f32x4 *)&Ks[r * KSTR + 4 * c4] = kv;
                 *(f32x4 *)&Vs[r * D + 4 * c4] = vv;
@@ -147,7 +180,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
         for (int kk = 0; kk < DH; kk += 4) {
 #pragma unroll
             for (int blk = 0; blk < kBc / 32; ++blk) {
-                const f32x4 kf = *(const f32x4 *)&Ks[(32 * blk + l32) * KSTR + h32 * DH + kk];
+                const f32x4 kf = *(const f32x4 *)&kslab[(32 * blk + l32) * KSTR + h32 * DH + kk];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) sacc[blk] = mfma_32x32x2(kf[j], qr[kk + j], sacc[blk]);
             }
@@ -215,7 +248,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int nr = 32 * blk + acc_row(i, h32);
-                const typename VecN<DB>::T vf = *(const typename VecN<DB>::T *)&Vs[nr * D + DB * l32];
+                const typename VecN<DB>::T vf = *(const typename VecN<DB>::T *)&vslab[nr * D + DB * l32];
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
                     oacc[db] = mfma_32x32x2(vget<DB>(vf, db), sacc[blk][i], oacc[db]);
@@ -224,7 +257,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
     }
 
     const float ltot = lrun + __shfl_xor(lrun, 32);
-    if (mq < S) {
+    if (mq < S && head_ok) {
         const float inv = 1.0f / ltot;
         float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss;
 #pragma unroll
@@ -244,9 +277,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(FwdArgs a)
 }
 
 template <int D, bool CAUSAL>
-int launch_fwd(const FwdArgs &args, int nblocks)
+int launch_fwd(FwdArgs args, int64_t nbh)
 {
-    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    if (args.S <= 32) {
+        args.nqb = 1;
+        const int nblocks = (int)((nbh + 3) / 4);
+        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, 4, 32>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    } else if (args.S <= 64) {
+        args.nqb = 1;
+        const int nblocks = (int)((nbh + 1) / 2);
+        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, 2, 64>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    } else {
+        args.nqb = (args.S + kBr - 1) / kBr;
+        const int nblocks = args.nqb * (int)nbh;
+        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, 1, 64>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    }
     return launch_ok("attn_fwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
@@ -294,7 +339,7 @@ extern "C" int attention_fwd(const float *q, const float *k, const float *v, flo
     args.lse = lse;
     args.H = (int)H;
     args.S = (int)S;
-    args.nqb = (int)((S + kBr - 1) / kBr);
+    args.nbh = (int)(B * H);
     args.c = scale * kLog2e;
     args.in_sb = in_sb;
     args.in_sh = in_sh;
@@ -302,13 +347,13 @@ extern "C" int attention_fwd(const float *q, const float *k, const float *v, flo
     args.out_sb = out_sb;
     args.out_sh = out_sh;
     args.out_ss = out_ss;
-    const int nblocks = args.nqb * (int)(B * H);
+    const int64_t nbh = B * H;
     switch (D * 2 + (causal ? 1 : 0)) {
-        case 64: return launch_fwd<32, false>(args, nblocks);
-        case 65: return launch_fwd<32, true>(args, nblocks);
-        case 128: return launch_fwd<64, false>(args, nblocks);
-        case 129: return launch_fwd<64, true>(args, nblocks);
-        case 256: return launch_fwd<128, false>(args, nblocks);
-        default: return launch_fwd<128, true>(args, nblocks);
+        case 64: return launch_fwd<32, false>(args, nbh);
+        case 65: return launch_fwd<32, true>(args, nbh);
+        case 128: return launch_fwd<64, false>(args, nbh);
+        case 129: return launch_fwd<64, true>(args, nbh);
+        case 256: return launch_fwd<128, false>(args, nbh);
+        default: return launch_fwd<128, true>(args, nbh);
     }
 }

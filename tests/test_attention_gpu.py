@@ -69,6 +69,23 @@ def test_fwd_bwd_edges_match_oracle(S, D, causal):
     np.testing.assert_allclose(dv, dv_r, **TOL)
 
 
+@pytest.mark.parametrize("B,H,S,D,causal", [(3, 3, 20, 64, True), (3, 3, 50, 128, False),
+                                           (1, 5, 32, 32, True), (2, 3, 64, 128, True),
+                                           (5, 1, 7, 128, False), (2, 7, 33, 64, False)])
+def test_short_sequences_pack_heads(B, H, S, D, causal):
+    """S <= 64 packs 2 or 4 heads into a workgroup; head counts that do not
+    fill the last workgroup must neither leak nor write past the last head."""
+    q, k, v, d_o = _inputs(B, H, S, D, seed=S + D + B * H)
+    o, lse = G.attention_fwd(q, k, v, causal)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, causal, G.scale_for(D))
+    np.testing.assert_allclose(o, o_ref, **TOL)
+    np.testing.assert_allclose(lse, lse_ref, **TOL)
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    refs = oracle.attention_bwd(q, k, v, o_ref, lse_ref, d_o, causal, G.scale_for(D))
+    for got, ref in zip((dq, dk, dv), refs):
+        np.testing.assert_allclose(got, ref, **TOL)
+
+
 def test_config1_forward_full():
     """B=1 H=4 S=256 D=64 non-causal: full O against the CPU path."""
     q, k, v, _ = _inputs(1, 4, 256, 64, seed=100)
