@@ -276,9 +276,196 @@ __global__ __launch_bounds__(kThreads, HP == 1 ? 2 : 1) void attn_fwd_kernel(Fwd
     }
 }
 
+// Split-key forward for launches too small to fill the GPU (few heads of
+// moderate length, config 1's shape): a workgroup owns 32 queries of one
+// head and its 4 waves walk interleaved 32-key tiles (wave w takes tiles
+// w, w+4, ...).  A wave loads its tile's K and V straight into registers in
+// MFMA operand order (no LDS, no barriers in the loop; the next tile's loads
+// are issued before the current tile's products), runs the same online
+// softmax as attn_fwd_kernel, and the four partial states are merged at the
+// end through LDS:  M = max_w m_w,  L = sum_w l_w 2^(m_w - M),
+// O = sum_w O_w 2^(m_w - M) / L.  A wave that sees no key ends with
+// m = -inf, l = 0, O = 0 and drops out of the merge; wave 0's first tile
+// holds key 0, visible to every query, so M is finite.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 1) void attn_fwd_split(FwdArgs a)
+{
+    constexpr int DH = D / 2;
+    constexpr int DB = D / 32;
+    typedef typename VecN<DB>::T VT;
+    __shared__ float part[kWaves * D * 32];  // O^T partials [w][d][query]
+    __shared__ float mst[kWaves * 32], lst[kWaves * 32];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+
+    const int nqb = a.nqb;  // 32-query blocks per head
+    const int bh = blockIdx.x / nqb;
+    const int qb = blockIdx.x - bh * nqb;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int m0 = 32 * qb;
+    const int mq = m0 + l32;
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+
+    float qr[DH];
+    {
+        const int mrow = mq < S ? mq : S - 1;
+        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + h32 * DH;
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            const f32x4 t = *(const f32x4 *)(src + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qr[kk + j] = t[j];
+        }
+    }
+
+    // K operand: lane holds K[n0 + l32][h32*DH + kk]; V operand for k-step i:
+    // V[n0 + acc_row(i, h32)][DB*l32 .. +DB).  Rows past S are clamped
+    // (their scores are masked).
+    float kr[DH];
+    VT vr[16];
+    auto load_tile = [&](int n0, float (&kd)[DH], VT (&vd)[16]) {
+        const int nk = n0 + l32 < S ? n0 + l32 : S - 1;
+        const float *ks = a.k + in_base + (int64_t)nk * a.in_ss + h32 * DH;
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            const f32x4 t = *(const f32x4 *)(ks + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kd[kk + j] = t[j];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int nv = n0 + acc_row(i, h32);
+            nv = nv < S ? nv : S - 1;
+            vd[i] = *(const VT *)(a.v + in_base + (int64_t)nv * a.in_ss + DB * l32);
+        }
+    };
+
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+    float mrun = -INFINITY, lrun = 0.0f;
+
+    const int kend = CAUSAL ? min(S, m0 + 32) : S;
+    const int ntiles = (kend + 31) / 32;
+    int t = w;
+    if (t < ntiles) load_tile(32 * t, kr, vr);
+    for (; t < ntiles; t += kWaves) {
+        const int n0 = 32 * t;
+        float kn[DH];
+        VT vn[16];
+        const bool more = t + kWaves < ntiles;
+        if (more) load_tile(n0 + 32 * kWaves, kn, vn);
+
+        f32x16 sacc = zero16();
+#pragma unroll
+        for (int kk = 0; kk < DH; ++kk) sacc = mfma_32x32x2(kr[kk], qr[kk], sacc);
+        if (n0 + 32 > S || (CAUSAL && n0 + 31 > m0)) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int n = n0 + acc_row(i, h32);
+                const bool vis = (n < S) & (!CAUSAL | (n <= mq));
+                sacc[i] = vis ? sacc[i] : -INFINITY;
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float tm2 = tmax * a.c;
+        // Same lazy rescaling as attn_fwd_kernel; a wave's first tile may be
+        // wholly masked for some queries (tm2 = -inf), which leaves mrun
+        // unchanged.
+        if (__ballot(tm2 > mrun + 8.0f) != 0) {
+            const float mnew = fmaxf(mrun, tm2);
+            const float alpha = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
+            mrun = mnew;
+            lrun *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float sv = sacc[i];
+            const float p = sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv, a.c, -mrun));
+            sacc[i] = p;
+            lrun += p;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) oacc[db] = mfma_32x32x2(vget<DB>(vr[i], db), sacc[i], oacc[db]);
+        if (more) {
+#pragma unroll
+            for (int kk = 0; kk < DH; ++kk) kr[kk] = kn[kk];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) vr[i] = vn[i];
+        }
+    }
+
+    // Publish this wave's state: m (in scaled log2 units), l, O^T.
+    const float ltot = lrun + __shfl_xor(lrun, 32);
+    if (h32 == 0) {
+        mst[w * 32 + l32] = mrun;
+        lst[w * 32 + l32] = ltot;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+            part[(w * D + DB * acc_row(i, h32) + db) * 32 + l32] = oacc[db][i];
+    __syncthreads();
+
+    // Merge: wave w writes d in [w*D/4, (w+1)*D/4) of query l32; lane half
+    // h32 takes the first or second half of that range.
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) M = fmaxf(M, mst[v * 32 + l32]);
+    float f[kWaves], L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) {
+        const float mv = mst[v * 32 + l32];
+        f[v] = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - M);
+        L += f[v] * lst[v * 32 + l32];
+    }
+    if (mq < S) {
+        const float inv = 1.0f / L;
+        constexpr int DQ = D / 8;  // d values per lane
+        const int d0 = w * (D / 4) + h32 * DQ;
+        float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss + d0;
+#pragma unroll
+        for (int d4 = 0; d4 < DQ; d4 += 4) {
+            f32x4 o4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int v = 0; v < kWaves; ++v) acc += f[v] * part[(v * D + d0 + d4 + j) * 32 + l32];
+                o4[j] = acc * inv;
+            }
+            *(f32x4 *)(orow + d4) = o4;
+        }
+        if (w == 0 && h32 == 0) a.lse[(int64_t)bh * S + mq] = (M + log2f(L)) * kLn2;
+    }
+}
+
 template <int D, bool CAUSAL>
 int launch_fwd(FwdArgs args, int64_t nbh)
 {
+    // A launch that would leave most CUs idle (and is longer than the
+    // packed short-sequence case) splits the keys across waves instead.
+    const int64_t regular = (args.S + kBr - 1) / kBr * nbh;
+    if (args.S > 64 && regular * 4 <= 256) {
+        args.nqb = (args.S + 31) / 32;
+        hipLaunchKernelGGL((attn_fwd_split<D, CAUSAL>), dim3((unsigned)(args.nqb * nbh)), dim3(kThreads),
+                           0, 0, args);
+        return launch_ok("attn_fwd_split") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
     if (args.S <= 32) {
         args.nqb = 1;
         const int nblocks = (int)((nbh + 3) / 4);

@@ -86,6 +86,19 @@ def test_short_sequences_pack_heads(B, H, S, D, causal):
         np.testing.assert_allclose(got, ref, **TOL)
 
 
+@pytest.mark.parametrize("B,H,S,D,causal", [(4, 20, 257, 64, True), (2, 40, 129, 128, False),
+                                           (4, 17, 200, 32, True), (3, 30, 300, 128, True)])
+def test_full_width_launches_with_ragged_length(B, H, S, D, causal):
+    """Enough heads that the forward takes its one-head-per-workgroup path
+    (small launches split the keys across waves instead, covered by the
+    edge cases above), with S not a multiple of the 128-query block."""
+    q, k, v, d_o = _inputs(B, H, S, D, seed=S + H)
+    o, lse = G.attention_fwd(q, k, v, causal)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, causal)
+    np.testing.assert_allclose(o, o_ref, **TOL)
+    np.testing.assert_allclose(lse, lse_ref, **TOL)
+
+
 def test_config1_forward_full():
     """B=1 H=4 S=256 D=64 non-causal: full O against the CPU path."""
     q, k, v, _ = _inputs(1, 4, 256, 64, seed=100)
