@@ -271,7 +271,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    // Wave index made provably uniform: the per-wave copy counts and LDS
+    // destinations below then use scalar branches and registers.
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
     const int wr = w >> 1, wc = w & 1;
@@ -403,8 +405,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
     // Output: row(rb, i) and col(cb) as the operand layouts above define them.
     const int64_t zoff = SPLIT ? ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * g.sc
                                : (int64_t)blockIdx.y * g.sc;
-    float *C = (SPLIT ? g.part : g.c) + zoff + (int64_t)row0 * g.m + col0;
+    const int64_t tile_off = zoff + (int64_t)row0 * g.m + col0;
+    float *C = (SPLIT ? g.part : g.c) + tile_off;
     const bool epi = !SPLIT && (g.bias || g.pre || g.act || g.residual);
+    // This lane's output columns (within the tile) for accumulator column
+    // block cb: 4*l32 + cb (+128*wc) in the normal layout, 32*cb + l32 with
+    // b transposed.  The epilogue's bias is loaded once per column.
+    auto colof = [&](int cb) { return 128 * wc + (TB ? 32 * cb + l32 : 4 * l32 + cb); };
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (epi && g.bias) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) bv[cb] = g.bias[col0 + colof(cb)];
+    }
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
@@ -413,25 +425,32 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
             f32x4 v;
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) v[cb] = acc[rb][cb][i];
+            const int64_t roff = (int64_t)row * g.m;
+            if (epi) {
+                // out = act(acc + bias) + residual, pre = acc + bias.
+#pragma clang fp contract(off)
+                if (g.bias) v += bv;
+                if (TB) {
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        if (g.pre) g.pre[tile_off + roff + colof(cb)] = v[cb];
+                        if (g.act == 1) v[cb] = gelu08(v[cb]);
+                        if (g.residual) v[cb] += g.residual[tile_off + roff + colof(cb)];
+                    }
+                } else {
+                    if (g.pre) *(f32x4 *)&g.pre[tile_off + roff + colof(0)] = v;
+                    if (g.act == 1) {
+#pragma unroll
+                        for (int cb = 0; cb < 4; ++cb) v[cb] = gelu08(v[cb]);
+                    }
+                    if (g.residual) v += *(const f32x4 *)&g.residual[tile_off + roff + colof(0)];
+                }
+            }
             if (TB) {
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) {
-                    const int col = 128 * wc + 32 * cb + l32;
-                    float x = v[cb];
-                    if (epi) {
-                        const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)(row0 + row) * g.m + col0 + col;
-                        x = epilogue(g, x, off, col0 + col);
-                    }
-                    C[(int64_t)row * g.m + col] = x;
-                }
+                for (int cb = 0; cb < 4; ++cb) C[roff + colof(cb)] = v[cb];
             } else {
-                const int col = 128 * wc + 4 * l32;
-                if (epi) {
-                    const int64_t off = (int64_t)blockIdx.y * g.sc + (int64_t)(row0 + row) * g.m + col0 + col;
-#pragma unroll
-                    for (int cb = 0; cb < 4; ++cb) v[cb] = epilogue(g, v[cb], off + cb, col0 + col + cb);
-                }
-                *(f32x4 *)&C[(int64_t)row * g.m + col] = v;
+                *(f32x4 *)&C[roff + colof(0)] = v;
             }
         }
     }
@@ -514,7 +533,9 @@ int gemm_launch(const float *a, const float *b, float *out, int batch, int n, in
     if (batch > 65535) return record_error(EMBER_ERR_UNSUPPORTED, who);
     const bool vec = (k % 4 == 0) && (m % 4 == 0) && (n % 4 == 0 || !ta) &&
                      (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
-    if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 && ((uintptr_t)out % 16) == 0) {
+    // The fast kernel moves out, pre and residual as 16-byte vectors.
+    if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 &&
+        (((uintptr_t)out | (uintptr_t)pre | (uintptr_t)residual) % 16) == 0) {
         g.tiles_n = n / FM;
         g.tiles_m = m / FN;
         const int work = g.tiles_n * g.tiles_m * batch;
