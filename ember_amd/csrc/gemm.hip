@@ -252,20 +252,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(GemmArgs g)
 constexpr int FM = 128, FN = 256, FK = 16;
 constexpr int FASTR = FK + 4;  // padded row of a k-contiguous slab
 
-template <bool TA> struct ASlab {
-    static constexpr int kBuf = TA ? FK * FM : FM * FASTR;     // floats
-    static constexpr int kCopies = TA ? kBuf / 256 : kBuf / 256;  // 1 KiB copies: 8 / 10
+template <bool TA, int TM = FM> struct ASlab {
+    static_assert(!TA || TM == 128, "a stored k x n: one 1 KiB copy is two 128-float rows");
+    static constexpr int kBuf = TA ? FK * TM : TM * FASTR;     // floats
+    static constexpr int kCopies = kBuf / 256;                  // 1 KiB copies
 };
 template <bool TB> struct BSlab {
     static constexpr int kBuf = TB ? FN * FASTR : FK * FN;
     static constexpr int kCopies = kBuf / 256;                  // 20 / 16
 };
 
-template <bool TA, bool TB, bool SPLIT>
-__global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
+// TM = 128 (4 waves, 2 workgroups per CU) or 256 (8 waves, 1 per CU: the
+// same 64 x 128 per wave, a third less L2 -> LDS traffic per flop).
+template <bool TA, bool TB, bool SPLIT, int TM = FM>
+__global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel(GemmArgs g)
 {
-    constexpr int ABUF = ASlab<TA>::kBuf, BBUF_ = BSlab<TB>::kBuf;
-    constexpr int ACOP = ASlab<TA>::kCopies, BCOP = BSlab<TB>::kCopies;
+    constexpr int NW = TM / 32;  // waves: TM/64 rows x 2 columns of 64 x 128
+    constexpr int ABUF = ASlab<TA, TM>::kBuf, BBUF_ = BSlab<TB>::kBuf;
+    constexpr int ACOP = ASlab<TA, TM>::kCopies, BCOP = BSlab<TB>::kCopies;
     __shared__ float As0[ABUF], As1[ABUF];
     __shared__ float Bs0[BBUF_], Bs1[BBUF_];
 
@@ -287,7 +291,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
     const int first = grp * GROUP;
     const int rows_in_grp = min(GROUP, g.tiles_n - first);
     const int in_grp = tile - grp * per_group;
-    const int row0 = (first + in_grp % rows_in_grp) * FM;
+    const int row0 = (first + in_grp % rows_in_grp) * TM;
     const int col0 = (in_grp / rows_in_grp) * FN;
 
     int kbeg = 0, kend = g.k;
@@ -300,11 +304,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
     const float *B = g.b + (int64_t)blockIdx.y * g.sb + (TB ? (int64_t)col0 * g.ldb : (int64_t)col0);
 
     // Per-lane offsets of the 1 KiB copies this wave issues (copy t = w + 4s).
-    constexpr int AS = (ACOP + 3) / 4, BS = (BCOP + 3) / 4;
+    constexpr int AS = (ACOP + NW - 1) / NW, BS = (BCOP + NW - 1) / NW;
     unsigned aoff[AS], boff[BS];
 #pragma unroll
     for (int s = 0; s < AS; ++s) {
-        const int t = w + 4 * s;
+        const int t = w + NW * s;
         if (TA) {  // copy t: k-rows 2t, 2t+1, 32 chunks each
             aoff[s] = (unsigned)((2 * t + h32) * g.lda + 4 * l32);
         } else {   // row p / 5, chunk p % 5 (chunk 4 is row padding: re-read chunk 0)
@@ -315,7 +319,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
     }
 #pragma unroll
     for (int s = 0; s < BS; ++s) {
-        const int t = w + 4 * s;
+        const int t = w + NW * s;
         if (TB) {
             const int p = 64 * t + lane;
             const int r = p / (FASTR / 4), c = p - r * (FASTR / 4);
@@ -330,10 +334,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
         const float *Bk = TB ? B + k0 : B + (int64_t)k0 * g.ldb;
 #pragma unroll
         for (int s = 0; s < AS; ++s)
-            if (w + 4 * s < ACOP) dma16(Ak + aoff[s], as + 256 * (w + 4 * s));
+            if (w + NW * s < ACOP) dma16(Ak + aoff[s], as + 256 * (w + NW * s));
 #pragma unroll
         for (int s = 0; s < BS; ++s)
-            if (w + 4 * s < BCOP) dma16(Bk + boff[s], bs + 256 * (w + 4 * s));
+            if (w + NW * s < BCOP) dma16(Bk + boff[s], bs + 256 * (w + NW * s));
     };
 
     f32x16 acc[2][4];
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
 
-    const int abase = TA ? 8 * h32 * FM + 64 * wr + 2 * l32 : (64 * wr + l32) * FASTR + 8 * h32;
+    const int abase = TA ? 8 * h32 * TM + 64 * wr + 2 * l32 : (64 * wr + l32) * FASTR + 8 * h32;
     const int bbase = TB ? (128 * wc + l32) * FASTR + 8 * h32 : 8 * h32 * FN + 128 * wc + 4 * l32;
     auto slab = [&](const float *__restrict__ as, const float *__restrict__ bs) {
 #pragma unroll
@@ -351,7 +355,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_dma_kernel(GemmArgs g)
             if (TA) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const f32x2 v = *(const f32x2 *)&as[abase + (kk + j) * FM];
+                    const f32x2 v = *(const f32x2 *)&as[abase + (kk + j) * TM];
                     af[0][j] = v[0];
                     af[1][j] = v[1];
                 }
@@ -495,6 +499,22 @@ int num_cus()
 template <bool TA, bool TB>
 void launch_fast(const GemmArgs &g, dim3 grid, bool split)
 {
+    // 256-row tiles when their count fills whole waves of CUs (or leaves a
+    // small tail): a 256 x 256 tile per CU reads a third less per flop, but
+    // a partly idle last wave costs more than that saves.
+    if constexpr (!TA) {
+        if (!split && g.n % 256 == 0) {
+            const int cus = num_cus();
+            const int tiles = (g.n / 256) * g.tiles_m * (int)grid.y;
+            if (tiles % cus == 0 || tiles >= 4 * cus) {
+                GemmArgs g2 = g;
+                g2.tiles_n = g.n / 256;
+                const dim3 grid2(g2.tiles_n * g2.tiles_m, grid.y, 1);
+                hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, false, 256>), grid2, dim3(512), 0, 0, g2);
+                return;
+            }
+        }
+    }
     if (split)
         hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, true>), grid, dim3(kThreads), 0, 0, g);
     else

@@ -128,3 +128,26 @@ def test_gemm_ex_epilogue_with_and_without_split(n, k, m):
     y, pre = G.gemm_ex(a, _stored(b, True), False, True, bias=bias, act=1)
     assert (np.abs(pre - (exact + bias)) <= bound + 1e-6 * (1 + np.abs(exact))).all()
     np.testing.assert_allclose(y, oracle.gelu_fwd(pre), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n,k,m,tb", [(4096, 64, 4096, False), (4096, 48, 4096, True),
+                                      (16384, 32, 3072, False)])
+def test_gemm_256_row_tiles(n, k, m, tb):
+    """Outputs whose 256 x 256 tiles fill whole waves of CUs take the 8-wave
+    kernel (256-row tiles)."""
+    a, b = _u((n, k), 11), _u((k, m), 12)
+    _check(G.gemm_ex(a, _stored(b, tb), False, tb), a, b)
+
+
+def test_gemm_256_row_tiles_epilogue():
+    n, k, m = 4096, 32, 4096
+    a, b = _u((n, k), 13), _u((k, m), 14)
+    bias, res = _u((m,), 15), _u((n, m), 16)
+    exact = oracle.matmul(a, b, threads=True).astype(np.float64)
+    bound = G.gemm_error_bound(a, b)
+    got = G.gemm_ex(a, b, bias=bias, residual=res)
+    ref = exact + bias + res
+    assert (np.abs(got - ref) <= bound + 1e-6 * (1 + np.abs(ref))).all()
+    y, pre = G.gemm_ex(a, b, bias=bias, act=1)
+    assert (np.abs(pre - (exact + bias)) <= bound + 1e-6 * (1 + np.abs(exact))).all()
+    np.testing.assert_allclose(y, oracle.gelu_fwd(pre), rtol=1e-5, atol=1e-6)
