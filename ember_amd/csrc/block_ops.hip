@@ -6,9 +6,14 @@
 //             (ember/nn/activations.py:61-66, evaluated in the order of
 //             Ember's element-wise operators; u = GELU input, y = output)
 //   col_sum:  out[c] = sum_r x[r][c], the bias gradient of a Linear layer
-//             (ember/nn/layers.py:53, em.sum(grad_y, axis=0)); two launches,
-//             per-slice partial sums then their sum in slice order, so the
-//             result is deterministic.
+//             (ember/nn/layers.py:54, em.sum(grad_y, axis=0)).  Widths that
+//             are a multiple of 4 (16-byte aligned): a workgroup owns 64
+//             columns (16 float4 quads) of a 256-row slice and 16 row groups
+//             sum interleaved rows, then the groups are added in order; a
+//             second launch reduces the slice partials the same way.  Other
+//             widths: one thread per column over 128-row slices, then the
+//             slices in order.  Either way the order is fixed, so the result
+//             is deterministic.
 // Both HBM-bound.
 #include <math.h>
 
@@ -46,6 +51,42 @@ __global__ __launch_bounds__(256) void col_sum_partial(const float *__restrict__
     part[(int64_t)blockIdx.y * cols + c] = s;
 }
 
+// out[y][c] = sum over rows r in [y*rpw, (y+1)*rpw) of x[r][c], c in quads.
+constexpr int kQuads = 16, kGroups = 16, kSliceRows = 256;
+__global__ __launch_bounds__(256) void col_reduce4(const float *__restrict__ x, float *__restrict__ out,
+                                                   int64_t rows, int cols, int rpw)
+{
+    __shared__ float4 red[kGroups][kQuads];
+    const int q = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
+    const int quad = blockIdx.x * kQuads + q;
+    const int64_t r0 = (int64_t)blockIdx.y * rpw;
+    const int64_t r1 = r0 + rpw < rows ? r0 + rpw : rows;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (4 * quad < cols) {
+        for (int64_t r = r0 + g; r < r1; r += kGroups) {
+            const float4 v = *(const float4 *)(x + r * cols + 4 * quad);
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+    }
+    red[g][q] = s;
+    __syncthreads();
+    if (g == 0 && 4 * quad < cols) {
+        float4 t = red[0][q];
+#pragma unroll
+        for (int gg = 1; gg < kGroups; ++gg) {
+            const float4 u = red[gg][q];
+            t.x += u.x;
+            t.y += u.y;
+            t.z += u.z;
+            t.w += u.w;
+        }
+        *(float4 *)(out + (int64_t)blockIdx.y * cols + 4 * quad) = t;
+    }
+}
+
 __global__ __launch_bounds__(256) void col_sum_final(const float *__restrict__ part,
                                                      float *__restrict__ out, int slices, int cols)
 {
@@ -77,6 +118,24 @@ extern "C" int col_sum(const float *x, float *out, int64_t rows, int64_t cols)
     if (rows < 0 || cols < 0 || cols > INT32_MAX) return record_error(EMBER_ERR_INVALID_ARGUMENT, "col_sum");
     if (cols == 0) return EMBER_OK;
     if (!out || (rows > 0 && !x)) return record_error(EMBER_ERR_INVALID_ARGUMENT, "col_sum");
+    if (rows > 0 && cols % 4 == 0 && (((uintptr_t)x | (uintptr_t)out) % 16) == 0) {
+        const unsigned cblocks = (unsigned)((cols / 4 + kQuads - 1) / kQuads);
+        const int64_t slices4 = (rows + kSliceRows - 1) / kSliceRows;
+        if (slices4 > 65535) return record_error(EMBER_ERR_UNSUPPORTED, "col_sum");
+        if (slices4 == 1) {
+            hipLaunchKernelGGL(col_reduce4, dim3(cblocks, 1), dim3(256), 0, 0, x, out, rows, (int)cols,
+                               (int)rows);
+            return launch_ok("col_reduce4") ? EMBER_OK : EMBER_ERR_DEVICE;
+        }
+        float *part4 = (float *)scratch(kScratchColSum, (size_t)slices4 * cols * sizeof(float));
+        if (!part4) return EMBER_ERR_OUT_OF_MEMORY;
+        hipLaunchKernelGGL(col_reduce4, dim3(cblocks, (unsigned)slices4), dim3(256), 0, 0, x, part4,
+                           rows, (int)cols, kSliceRows);
+        if (!launch_ok("col_reduce4")) return EMBER_ERR_DEVICE;
+        hipLaunchKernelGGL(col_reduce4, dim3(cblocks, 1), dim3(256), 0, 0, (const float *)part4, out,
+                           slices4, (int)cols, (int)slices4);
+        return launch_ok("col_reduce4") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
     const int64_t slices = (rows + kRowsPerSlice - 1) / kRowsPerSlice;
     if (slices > 65535) return record_error(EMBER_ERR_UNSUPPORTED, "col_sum");
     float *part = nullptr;

@@ -6,15 +6,18 @@
 //   mean = sum(x)/d;  var = sum((x - mean)^2)/d  (biased);
 //   rstd = 1/sqrt(var + eps);  y = (x - mean)*rstd*gamma + beta
 //   backward (xhat = (x - mean)*rstd, g = dy*gamma):
-//   dx = rstd*(g - mean(g) - xhat*mean(g*xhat));
+//   dx = rstd*(g - mean(g) - xhat*mean(g*xhat))  (+ dres, the gradient that
+//        reaches x through a residual connection, when given);
 //   dgamma = sum_rows(dy*xhat);  dbeta = sum_rows(dy)
 //
 // HBM-bound.  One wave per row; a row is held in registers (d <= 4096, a
 // multiple of 4) as 16-byte chunks, 64 lanes wide, so x is read once; the
-// row reductions are wave shuffles.  dgamma / dbeta: each workgroup sums its
-// rows' contributions per column in registers and writes one partial row;
-// a second launch adds the partials in a fixed order (deterministic, no
-// atomics).  The partials live in library scratch.
+// row reductions are wave shuffles.  dgamma / dbeta: each workgroup (8 rows,
+// so that ~1000 workgroups keep the loads in flight) sums its rows'
+// contributions per column in registers and writes one partial row; a second
+// launch adds the partials in a fixed tree order (16 interleaved runs per
+// column, then the runs in order: deterministic, no atomics).  The partials
+// live in library scratch.
 #include <math.h>
 
 #include "common.h"
@@ -92,6 +95,7 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const float *__restric
                                                          const float *__restrict__ mean_in,
                                                          const float *__restrict__ rstd_in,
                                                          const float *__restrict__ dy,
+                                                         const float *__restrict__ dres,
                                                          float *__restrict__ dx,
                                                          float *__restrict__ part, int64_t rows,
                                                          int d, int rows_per_block)
@@ -142,6 +146,13 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const float *__restric
                 o.y = rstd * (gg[c].y - m1 - xh[c].y * m2);
                 o.z = rstd * (gg[c].z - m1 - xh[c].z * m2);
                 o.w = rstd * (gg[c].w - m1 - xh[c].w * m2);
+                if (dres) {
+                    const float4 r = *(const float4 *)(dres + row * d + col);
+                    o.x += r.x;
+                    o.y += r.y;
+                    o.z += r.z;
+                    o.w += r.w;
+                }
                 *(float4 *)(dx + row * d + col) = o;
             }
         }
@@ -174,18 +185,46 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const float *__restric
     }
 }
 
-// dgamma[c] = sum_b part[b][0][c], dbeta[c] = sum_b part[b][1][c], b in order.
+// dgamma[c] = sum_b part[b][0][c], dbeta[c] = sum_b part[b][1][c]: a
+// workgroup owns 16 quads of the 2d output columns; thread group g (of 16)
+// sums partial rows b = g, g+16, ... in order (float4), then the 16 group
+// sums are added in g order.
+constexpr int kPgQuads = 16, kPgGroups = 16;
 __global__ __launch_bounds__(256) void ln_param_grad_kernel(const float *__restrict__ part,
                                                             float *__restrict__ dgamma,
                                                             float *__restrict__ dbeta, int nblk,
                                                             int d)
 {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= 2 * d) return;
-    const int which = c / d, col = c - which * d;
-    float s = 0.0f;
-    for (int b = 0; b < nblk; ++b) s += part[((int64_t)b * 2 + which) * d + col];
-    (which ? dbeta : dgamma)[col] = s;
+    __shared__ float4 red[kPgGroups][kPgQuads];
+    const int q = threadIdx.x % kPgQuads, g = threadIdx.x / kPgQuads;
+    const int quad = blockIdx.x * kPgQuads + q;  // over 2d/4 column quads
+    const int nq = 2 * d / 4;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (quad < nq) {
+        const int which = (4 * quad) / d, col = 4 * quad - which * d;
+        for (int b = g; b < nblk; b += kPgGroups) {
+            const float4 v = *(const float4 *)(part + ((int64_t)b * 2 + which) * d + col);
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+    }
+    red[g][q] = s;
+    __syncthreads();
+    if (g == 0 && quad < nq) {
+        float4 t = red[0][q];
+#pragma unroll
+        for (int gg = 1; gg < kPgGroups; ++gg) {
+            const float4 u = red[gg][q];
+            t.x += u.x;
+            t.y += u.y;
+            t.z += u.z;
+            t.w += u.w;
+        }
+        const int which = (4 * quad) / d, col = 4 * quad - which * d;
+        *(float4 *)((which ? dbeta : dgamma) + col) = t;
+    }
 }
 
 // Status of the argument checks (pointers are checked even for rows == 0).
@@ -210,10 +249,11 @@ void launch_fwd(const float *x, const float *g, const float *b, float *y, float 
 
 template <int NC>
 void launch_bwd(const float *x, const float *g, const float *mean, const float *rstd,
-                const float *dy, float *dx, float *part, int64_t rows, int d, int rpb, int nblk)
+                const float *dy, const float *dres, float *dx, float *part, int64_t rows, int d,
+                int rpb, int nblk)
 {
-    hipLaunchKernelGGL(ln_bwd_kernel<NC>, dim3(nblk), dim3(kThreads), 0, 0, x, g, mean, rstd, dy, dx,
-                       part, rows, d, rpb);
+    hipLaunchKernelGGL(ln_bwd_kernel<NC>, dim3(nblk), dim3(kThreads), 0, 0, x, g, mean, rstd, dy,
+                       dres, dx, part, rows, d, rpb);
 }
 
 }  // namespace
@@ -239,34 +279,37 @@ extern "C" int layernorm_fwd(const float *x, const float *gamma, const float *be
 }
 
 extern "C" int layernorm_bwd(const float *x, const float *gamma, const float *mean,
-                             const float *rstd, const float *dy, float *dx, float *dgamma,
-                             float *dbeta, int64_t rows, int64_t d)
+                             const float *rstd, const float *dy, const float *dres, float *dx,
+                             float *dgamma, float *dbeta, int64_t rows, int64_t d)
 {
     using namespace ember;
     const void *ptrs[] = {x, gamma, mean, rstd, dy, dx, dgamma, dbeta};
     const int st = ln_args(ptrs, 8, rows, d, "layernorm_bwd");
     if (st != EMBER_OK) return st;
+    if ((uintptr_t)dres & 15) return record_error(EMBER_ERR_INVALID_ARGUMENT, "layernorm_bwd");
+    const unsigned pg_blocks = (unsigned)((2 * d / 4 + kPgQuads - 1) / kPgQuads);
     if (rows == 0) {
         // Sums over no rows: the reduction kernel over zero partials writes 0.
-        hipLaunchKernelGGL(ln_param_grad_kernel, dim3((unsigned)((2 * d + 255) / 256)), dim3(256), 0,
-                           0, (const float *)nullptr, dgamma, dbeta, 0, (int)d);
+        hipLaunchKernelGGL(ln_param_grad_kernel, dim3(pg_blocks), dim3(256), 0, 0,
+                           (const float *)nullptr, dgamma, dbeta, 0, (int)d);
         return launch_ok("ln_param_grad_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
-    // About 256 workgroups (one per CU), each owning a contiguous run of rows.
-    const int64_t rpb64 = (rows + 255) / 256;
-    const int rpb = (int)(rpb64 < kWaves ? kWaves : rpb64);
+    // Workgroups of 8 rows (2 per wave), each owning a contiguous run; rows
+    // beyond 2^18 take longer runs so the partials stay under 2^15 rows.
+    const int64_t rpb64 = (rows + 32767) / 32768;
+    const int rpb = (int)(rpb64 < 2 * kWaves ? 2 * kWaves : rpb64);
     const int nblk = (int)((rows + rpb - 1) / rpb);
     float *part = (float *)scratch(kScratchLayerNorm, (size_t)nblk * 2 * d * sizeof(float));
     if (!part) return EMBER_ERR_OUT_OF_MEMORY;
     const int nc = (int)((d + 255) / 256);
     if (nc <= 4)
-        launch_bwd<4>(x, gamma, mean, rstd, dy, dx, part, rows, (int)d, rpb, nblk);
+        launch_bwd<4>(x, gamma, mean, rstd, dy, dres, dx, part, rows, (int)d, rpb, nblk);
     else if (nc <= 8)
-        launch_bwd<8>(x, gamma, mean, rstd, dy, dx, part, rows, (int)d, rpb, nblk);
+        launch_bwd<8>(x, gamma, mean, rstd, dy, dres, dx, part, rows, (int)d, rpb, nblk);
     else
-        launch_bwd<16>(x, gamma, mean, rstd, dy, dx, part, rows, (int)d, rpb, nblk);
+        launch_bwd<16>(x, gamma, mean, rstd, dy, dres, dx, part, rows, (int)d, rpb, nblk);
     if (!launch_ok("ln_bwd_kernel")) return EMBER_ERR_DEVICE;
-    hipLaunchKernelGGL(ln_param_grad_kernel, dim3((unsigned)((2 * d + 255) / 256)), dim3(256), 0, 0,
-                       part, dgamma, dbeta, nblk, (int)d);
+    hipLaunchKernelGGL(ln_param_grad_kernel, dim3(pg_blocks), dim3(256), 0, 0, part, dgamma, dbeta,
+                       nblk, (int)d);
     return launch_ok("ln_param_grad_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
 }

@@ -806,16 +806,21 @@ static PyObject *py_layernorm_fwd(PyObject *module, PyObject *args)
     return Py_BuildValue("(NNN)", (PyObject *)y, (PyObject *)mean, (PyObject *)rstd);
 }
 
+/* _layernorm_bwd(x, gamma, mean, rstd, dy, rows, d[, dres]) -> (dx, dgamma, dbeta);
+ * dres (optional) is added to dx: the gradient reaching x through a residual. */
 static PyObject *py_layernorm_bwd(PyObject *module, PyObject *args)
 {
     TensorObject *x, *g, *mean, *rstd, *dy;
+    PyObject *ro = Py_None;
     long long rows, d;
     (void)module;
-    if (!PyArg_ParseTuple(args, "O!O!O!O!O!LL", &TensorType, &x, &TensorType, &g, &TensorType, &mean,
-                          &TensorType, &rstd, &TensorType, &dy, &rows, &d))
+    if (!PyArg_ParseTuple(args, "O!O!O!O!O!LL|O", &TensorType, &x, &TensorType, &g, &TensorType,
+                          &mean, &TensorType, &rstd, &TensorType, &dy, &rows, &d, &ro))
         return NULL;
+    TensorObject *res = opt_tensor(ro, "dres");
+    if (res == (TensorObject *)-1) return NULL;
     if (rows < 0 || d <= 0 || x->size != (Py_ssize_t)(rows * d) || dy->size != x->size ||
-        g->size != d || mean->size != rows || rstd->size != rows) {
+        g->size != d || mean->size != rows || rstd->size != rows || (res && res->size != x->size)) {
         PyErr_SetString(PyExc_ValueError, "_layernorm_bwd: size mismatch");
         return NULL;
     }
@@ -825,8 +830,8 @@ static PyObject *py_layernorm_bwd(PyObject *module, PyObject *args)
         Py_XDECREF(dg);
         return NULL;
     }
-    int st = layernorm_bwd(x->d_ptr, g->d_ptr, mean->d_ptr, rstd->d_ptr, dy->d_ptr, dx->d_ptr,
-                           dg->d_ptr, db->d_ptr, rows, d);
+    int st = layernorm_bwd(x->d_ptr, g->d_ptr, mean->d_ptr, rstd->d_ptr, dy->d_ptr,
+                           res ? res->d_ptr : NULL, dx->d_ptr, dg->d_ptr, db->d_ptr, rows, d);
     if (raise_status(st, "_layernorm_bwd")) {
         Py_DECREF(dx);
         Py_DECREF(dg);

@@ -254,12 +254,15 @@ class LayerNorm(Layer):
         self._stats = (mean, rstd)
         return Tensor._from_core(y, x.shape)
 
-    def backward(self, grad_y: Tensor) -> Tensor:
+    def backward(self, grad_y: Tensor, residual: Tensor | None = None) -> Tensor:
+        """Gradient with respect to x; ``residual`` (the gradient reaching x
+        through a skip connection) is added in the same pass."""
         if self.x is None or self._stats is None:
             raise RuntimeError("forward() must run before backward()")
         d = self.x.shape[-1]
         dx, dg, db = C._layernorm_bwd(self.x._core, self.gamma._core, *self._stats, grad_y._core,
-                                      self.x.size // d, d)
+                                      self.x.size // d, d,
+                                      None if residual is None else residual._core)
         self.grad_gamma = Tensor._from_core(dg, (d,))
         self.grad_beta = Tensor._from_core(db, (d,))
         return Tensor._from_core(dx, self.x.shape)
@@ -335,7 +338,7 @@ class DecoderBlock(Layer):
         da = input_grad(grad_y, self.w_2)
         du = Tensor._from_core(C._gelu_bwd(da._core, u._core, a._core), da.shape)
         g_w1, g_b1 = weight_grad(h2, du), col_sum(du)
-        dx2 = self.ln2.backward(input_grad(du, self.w_1)) + grad_y
+        dx2 = self.ln2.backward(input_grad(du, self.w_1), residual=grad_y)
         # attention: x2 = x + O Wo + bo
         g_wo, g_bo = weight_grad(o, dx2), col_sum(dx2)
         d_o = input_grad(dx2, self.w_o)
@@ -343,7 +346,7 @@ class DecoderBlock(Layer):
             C._attention_bwd_packed(qkv._core, o._core, lse, d_o._core, B, S, self.h, D, scale,
                                     self.causal), qkv.shape)
         g_wqkv, g_bqkv = weight_grad(h1, dqkv), col_sum(dqkv)
-        dx = self.ln1.backward(input_grad(dqkv, self.w_qkv)) + dx2
+        dx = self.ln1.backward(input_grad(dqkv, self.w_qkv), residual=dx2)
         self._grads = [self.ln1.grad_gamma, self.ln1.grad_beta, g_wqkv, g_bqkv, g_wo, g_bo,
                        self.ln2.grad_gamma, self.ln2.grad_beta, g_w1, g_b1, g_w2, g_b2]
         return dx

@@ -190,13 +190,16 @@ int col_sum(const float *x, float *out, int64_t rows, int64_t cols);
  * 16-byte aligned and non-NULL):
  *   mean = sum(x)/d, var = sum((x-mean)^2)/d, rstd = 1/sqrt(var + eps),
  *   y = (x - mean)*rstd*gamma + beta;  mean and rstd (rows) are kept for
- * the backward, which gives dx and the parameter gradients
+ * the backward, which gives dx (plus dres when dres is not NULL: the gradient
+ * that reaches x through a residual connection, added in the same pass) and
+ * the parameter gradients
  *   dgamma = sum_rows(dy*xhat), dbeta = sum_rows(dy)   (xhat = (x-mean)*rstd)
  * deterministically (fixed-order reduction over library scratch). */
 int layernorm_fwd(const float *x, const float *gamma, const float *beta, float *y, float *mean,
                   float *rstd, int64_t rows, int64_t d, float eps);
 int layernorm_bwd(const float *x, const float *gamma, const float *mean, const float *rstd,
-                  const float *dy, float *dx, float *dgamma, float *dbeta, int64_t rows, int64_t d);
+                  const float *dy, const float *dres, float *dx, float *dgamma, float *dbeta,
+                  int64_t rows, int64_t d);
 
 #undef EMBER_BINARY_OP
 #undef EMBER_SCALAR_OP

@@ -18,7 +18,8 @@ def rnd(shape, seed, scale=1.0):
     return (scale * np.random.default_rng(seed).standard_normal(shape)).astype(np.float32)
 
 
-@pytest.mark.parametrize("rows,d", [(1, 64), (7, 1024), (1000, 1024), (33, 4096), (5, 100)])
+@pytest.mark.parametrize("rows,d", [(1, 64), (7, 1024), (1000, 1024), (33, 4096), (5, 100),
+                                    (8192, 1024), (70000, 64)])
 def test_layernorm_fwd_bwd(rows, d):
     G.say(f"layernorm rows={rows} d={d}")
     x = rnd((rows, d), 1, 2.0) + 0.5
@@ -33,6 +34,12 @@ def test_layernorm_fwd_bwd(rows, d):
     np.testing.assert_allclose(dx._to_np().reshape(rows, d), dx_ref, rtol=1e-4, atol=1e-5)
     np.testing.assert_allclose(dg._to_np(), dg_ref, rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(db._to_np(), db_ref, rtol=1e-4, atol=1e-4)
+    # the residual gradient is added to dx in the same pass
+    res = rnd((rows, d), 5)
+    dx2, dg2, db2 = _core._layernorm_bwd(Tensor(x)._core, Tensor(g)._core, mean, rstd, Tensor(dy)._core,
+                                         rows, d, Tensor(res)._core)
+    np.testing.assert_allclose(dx2._to_np().reshape(rows, d), dx_ref + res, rtol=1e-4, atol=1e-5)
+    np.testing.assert_array_equal(dg2._to_np(), dg._to_np())
 
 
 def test_layernorm_rejects_bad_widths():
@@ -67,7 +74,8 @@ def test_gelu_bwd_and_col_sum():
     dy = rnd((5000,), 12)
     dx = _core._gelu_bwd(Tensor(dy)._core, Tensor(u)._core, Tensor(a)._core)._to_np()
     np.testing.assert_allclose(dx, oracle.gelu_bwd(dy, u, a), rtol=1e-5, atol=1e-6)
-    for rows, cols in ((1, 7), (300, 1024), (8192, 3), (0, 5)):
+    for rows, cols in ((1, 7), (300, 1024), (8192, 3), (0, 5), (8192, 1024), (256, 64), (100000, 12),
+                       (257, 4096)):
         x = rnd((rows, cols), 13)
         got = nn.col_sum(Tensor(x) if rows else Tensor._from_core(_core._Tensor(0), (0, cols)))
         np.testing.assert_allclose(got.to_np(), x.astype(np.float64).sum(0), rtol=1e-5, atol=1e-4)
