@@ -48,9 +48,12 @@ struct FwdArgs {
 };
 
 // HP heads per workgroup (1, 2 or 4), each with 4/HP waves of 32 queries,
-// and key tiles of BC (64, or 32 when HP = 4).
+// and key tiles of BC (64, or 32 when HP = 4).  D = 64 asks for three
+// workgroups per CU (LDS allows it): its softmax costs twice the VALU
+// instructions per MFMA of D = 128, and a third wave per SIMD keeps the
+// matrix core fed while the other two run it.
 template <int D, bool CAUSAL, int HP, int BC>
-__global__ __launch_bounds__(kThreads, HP == 1 ? 2 : 1) void attn_fwd_kernel(FwdArgs a)
+__global__ __launch_bounds__(kThreads, HP == 1 ? (D == 64 ? 3 : 2) : 1) void attn_fwd_kernel(FwdArgs a)
 {
     constexpr int DH = D / 2;   // contraction length per lane half (k-steps)
     constexpr int DB = D / 32;  // 32-row blocks of O^T
