@@ -6,11 +6,15 @@
 //
 // Work decomposition.  One workgroup = 4 waves = 128 queries of one (b, h);
 // each wave owns 32 queries for the whole kernel.  The workgroup walks the
-// keys in tiles of 64: every tile of K and V is read from HBM once with
-// coalesced 128-bit loads and staged in LDS, where the 4 waves share it.
-// Short sequences pack heads instead: S <= 32 puts 4 heads in a workgroup
-// (one per wave, tiles of 32 keys) and S <= 64 puts 2 (two waves each), so
-// that no wave idles and the HBM-bound forward keeps every wave loading.
+// keys in tiles of 64: every tile of K and V is read from HBM once and
+// staged in LDS, where the 4 waves share it.  The copies go HBM -> LDS
+// directly (buffer_load_dwordx4 ... lds, no registers) and overlap the
+// products: V of tile t lands while S of tile t is computed, K of tile t+1
+// while V of tile t is multiplied; two barriers per tile.
+// Short sequences pack heads instead (attn_fwd_packed): S <= 32 puts 4
+// heads in a workgroup (one per wave, tiles of 32 keys) and S <= 64 puts 2
+// (two waves each), so that no wave idles and the HBM-bound forward keeps
+// every wave loading.
 //
 // Per tile and wave (all products on v_mfma_f32_32x32x2f32):
 //   S^T (64 keys x 32 queries) = K_tile . Q^T   -- K from LDS, Q^T resident in
@@ -28,6 +32,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "lds_dma.h"
 #include "mfma.h"
 
 namespace ember {
@@ -47,14 +52,287 @@ struct FwdArgs {
     int64_t in_sb, in_sh, in_ss, out_sb, out_sh, out_ss;
 };
 
-// HP heads per workgroup (1, 2 or 4), each with 4/HP waves of 32 queries,
-// and key tiles of BC (64, or 32 when HP = 4).  D = 64 asks for three
-// workgroups per CU (LDS allows it): its softmax costs twice the VALU
-// instructions per MFMA of D = 128, and a third wave per SIMD keeps the
-// matrix core fed while the other two run it.
-template <int D, bool CAUSAL, int HP, int BC>
-__global__ __launch_bounds__(kThreads, HP == 1 ? (D == 64 ? 3 : 2) : 1) void attn_fwd_kernel(FwdArgs a)
+// Copy layout of one 64-key tile for the direct HBM -> LDS copies.  A copy is
+// 64 lanes x 16 bytes = 1 KiB of LDS; copy t of a tile fills 16-byte chunks
+// 64t .. 64t+63.  K rows are padded to D+4 floats (conflict-free reads of a
+// column of chunks by 32 lanes): a padding chunk re-reads the tile's first
+// chunk (valid memory, never used).  V rows are dense.
+template <int D> struct FwdTile {
+    static constexpr int KSTR = D + 4;                       // floats per K row
+    static constexpr int KCH = KSTR / 4;                     // chunks per K row
+    static constexpr int KCOP = KCH;                         // copies per K tile: 64 rows * KCH / 64
+    static constexpr int VCOP = D / 4;                       // copies per V tile
+    static constexpr int KSL = (KCOP + kWaves - 1) / kWaves; // K copy slots per wave
+    static constexpr int VSL = VCOP / kWaves;                // V copy slots per wave
+    static constexpr int VROWS = kWaves * 256 / D;           // V rows between a wave's slots
+};
+
+// One head per workgroup, S > 64 (see the file comment).  Per tile t:
+//   wait for this wave's K copies, barrier (K(t) complete, Vs free)
+//   copy V(t) -> Vs;  S^T = K . Q^T;  mask, softmax
+//   wait for this wave's V copies, barrier (V(t) complete, Ks free)
+//   copy K(t+1) -> Ks;  O^T += V^T . P^T
+// A wave whose queries all precede the tile (causal) skips the products
+// but still issues its copies and meets both barriers.
+// Workgroups per CU: two, or three for non-causal D = 64 (LDS fits three
+// at D = 64; measured, the causal kernel runs best with two and the
+// non-causal one with three).
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd_kernel(FwdArgs a)
 {
+    typedef FwdTile<D> T;
+    constexpr int DH = D / 2;   // contraction length per lane half (k-steps)
+    constexpr int DB = D / 32;  // 32-row blocks of O^T
+    constexpr int KSTR = T::KSTR;
+    constexpr int kBc = 64;
+    // D = 128 keeps one offset register per V copy slot (it has the
+    // registers, and it saves the per-slot descriptor arithmetic); smaller D
+    // keeps one and moves the descriptor base per slot.
+    constexpr bool kVoffRegs = D == 128;
+    __shared__ float Ks[kBc * KSTR];
+    __shared__ float Vs[kBc * D];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+
+    // Heavy (late) query blocks first so the causal triangle load-balances.
+    const int BH = (int)(gridDim.x / a.nqb);
+    const int qbr = blockIdx.x / BH;
+    const int bh = blockIdx.x - qbr * BH;
+    const int qb = CAUSAL ? (a.nqb - 1 - qbr) : qbr;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int q0 = qb * kBr;
+    const int m0 = q0 + 32 * w;
+    const int mq = m0 + l32;
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int in_ss = (int)a.in_ss;  // < 2^24 (checked on the host)
+    const float *__restrict__ kbase = a.k + in_base;
+    const float *__restrict__ vbase = a.v + in_base;
+
+    // Byte offsets of this wave's copy slots within a tile (slot s is copy
+    // t = w + 4s, chunk p = 64t + lane).  Offsets stay below
+    // 64 * in_ss * 4 < 2^32.
+    int koff[T::KSL];
+#pragma unroll
+    for (int s = 0; s < T::KSL; ++s) {
+        const int p = 64 * (w + kWaves * s) + lane;
+        const int r = p / T::KCH, c = p - r * T::KCH;
+        koff[s] = c < D / 4 ? 4 * (r * in_ss + 4 * c) : 0;
+    }
+    int voff[kVoffRegs ? T::VSL : 1];
+#pragma unroll
+    for (int s = 0; s < (kVoffRegs ? T::VSL : 1); ++s) {
+        const int p = 64 * (w + kWaves * s) + lane;
+        const int r = p / (D / 4), c = p - r * (D / 4);
+        voff[s] = 4 * (r * in_ss + 4 * c);
+    }
+
+    // Rows past the sequence end re-read row S-1: their scores are masked,
+    // so they contribute exactly 0.  On that (last) tile the offsets are
+    // recomputed from an opaque lane index, so that the compiler does not
+    // keep a second set live across the loop.
+    auto fetch_k = [&](int n0) {
+        const __amdgpu_buffer_rsrc_t src = dma_rsrc(kbase + (int64_t)n0 * in_ss);
+        const int rmax = S - 1 - n0;
+        if (rmax >= kBc - 1) {
+#pragma unroll
+            for (int s = 0; s < T::KSL; ++s)
+                if (w + kWaves * s < T::KCOP) dma16_buf(src, (unsigned)koff[s], Ks + 256 * (w + kWaves * s));
+        } else {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+#pragma unroll
+            for (int s = 0; s < T::KSL; ++s) {
+                const int t = w + kWaves * s;
+                if (t < T::KCOP) {
+                    const int p = 64 * t + ln;
+                    const int r = p / T::KCH, c = p - r * T::KCH;
+                    const unsigned off = c < D / 4 ? 4u * (unsigned)(min(r, rmax) * in_ss + 4 * c) : 0u;
+                    dma16_buf(src, off, Ks + 256 * t);
+                }
+            }
+        }
+    };
+    auto fetch_v = [&](int n0) {
+        const int rmax = S - 1 - n0;
+        if (rmax >= kBc - 1) {
+#pragma unroll
+            for (int s = 0; s < T::VSL; ++s) {
+                if constexpr (kVoffRegs)
+                    dma16_buf(dma_rsrc(vbase + (int64_t)n0 * in_ss), (unsigned)voff[s],
+                              Vs + 256 * (w + kWaves * s));
+                else
+                    dma16_buf(dma_rsrc(vbase + (int64_t)(n0 + T::VROWS * s) * in_ss), (unsigned)voff[0],
+                              Vs + 256 * (w + kWaves * s));
+            }
+        } else {
+            const __amdgpu_buffer_rsrc_t src = dma_rsrc(vbase + (int64_t)n0 * in_ss);
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+#pragma unroll
+            for (int s = 0; s < T::VSL; ++s) {
+                const int t = w + kWaves * s;
+                const int p = 64 * t + ln;
+                const int r = p / (D / 4), c = p - r * (D / 4);
+                dma16_buf(src, 4u * (unsigned)(min(r, rmax) * in_ss + 4 * c), Vs + 256 * t);
+            }
+        }
+    };
+
+    const int kend = CAUSAL ? min(S, q0 + kBr) : S;
+    const int ntiles = (kend + kBc - 1) / kBc;
+    fetch_k(0);
+
+    // Q^T operand: lane holds Q[mq][h32*DH + kk] for k-step kk.
+    float qr[DH];
+    {
+        const int mrow = mq < S ? mq : S - 1;
+        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + h32 * DH;
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            f32x4 t = *(const f32x4 *)(src + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qr[kk + j] = t[j];
+        }
+    }
+
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+    float mrun = -INFINITY;  // reference max of s*c for query mq (see below)
+    float lrun = 0.0f;       // this lane half's share of the running sum
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int n0 = t * kBc;
+        wait_vmem();      // this wave's copies of K tile t have landed
+        __syncthreads();  // all of K tile t is in LDS; every wave is done with Vs
+        fetch_v(n0);
+        const bool active = !(CAUSAL && n0 > m0 + 31);  // some key at or before a query
+        f32x16 sacc[kBc / 32];
+        if (active) {
+            // S^T = K . Q^T for two 32-key blocks.
+#pragma unroll
+            for (int blk = 0; blk < kBc / 32; ++blk) sacc[blk] = zero16();
+#pragma unroll
+            for (int kk = 0; kk < DH; kk += 4) {
+#pragma unroll
+                for (int blk = 0; blk < kBc / 32; ++blk) {
+                    const f32x4 kf = *(const f32x4 *)&Ks[(32 * blk + l32) * KSTR + h32 * DH + kk];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) sacc[blk] = mfma_32x32x2(kf[j], qr[kk + j], sacc[blk]);
+                }
+            }
+
+            // Mask (diagonal and tail tiles only), tile max of the raw scores.
+            const bool need_mask = (n0 + kBc > S) || (CAUSAL && n0 + kBc - 1 > m0);
+            if (need_mask) {
+#pragma unroll
+                for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int n = n0 + 32 * blk + acc_row(i, h32);
+                        const bool vis = (n < S) & (!CAUSAL | (n <= mq));
+                        sacc[blk][i] = vis ? sacc[blk][i] : -INFINITY;
+                    }
+                }
+            }
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int blk = 0; blk < kBc / 32; ++blk)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[blk][i]);
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            // Scaled tile max (scale >= 0, checked on the host).  The
+            // reference max mrun is raised only when some lane's scores would
+            // otherwise exceed it by more than 2^8 (lazy rescaling): the
+            // result is the same softmax, and most tiles skip the rescale of
+            // O.  Tile 0 holds key 0, visible to every query, so it always
+            // sets a finite mrun.
+            const float tm2 = tmax * a.c;
+            if (__ballot(tm2 > mrun + 8.0f) != 0) {
+                const float mnew = fmaxf(mrun, tm2);
+                const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+                mrun = mnew;
+                lrun *= alpha;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+            }
+            if (need_mask) {
+#pragma unroll
+                for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float sv = sacc[blk][i];
+                        const float p = sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv, a.c, -mrun));
+                        sacc[blk][i] = p;
+                        lrun += p;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[blk][i], a.c, -mrun));
+                        sacc[blk][i] = p;
+                        lrun += p;
+                    }
+                }
+            }
+        }
+        wait_vmem();      // this wave's copies of V tile t have landed
+        __syncthreads();  // all of V tile t is in LDS; every wave is done with Ks
+        if (t + 1 < ntiles) fetch_k(n0 + kBc);
+        if (active) {
+            // O^T += V^T . P^T; lane l32 covers O^T rows d = DB*l32 + db.
+#pragma unroll
+            for (int blk = 0; blk < kBc / 32; ++blk) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int nr = 32 * blk + acc_row(i, h32);
+                    const typename VecN<DB>::T vf = *(const typename VecN<DB>::T *)&Vs[nr * D + DB * l32];
+#pragma unroll
+                    for (int db = 0; db < DB; ++db)
+                        oacc[db] = mfma_32x32x2(vget<DB>(vf, db), sacc[blk][i], oacc[db]);
+                }
+            }
+        }
+    }
+
+    const float ltot = lrun + __shfl_xor(lrun, 32);
+    if (mq < S) {
+        const float inv = 1.0f / ltot;
+        float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = acc_row(i, h32);  // O^T row block index -> d = DB*r + db
+            typename VecN<DB>::T outv;
+            if constexpr (DB == 1) {
+                outv = oacc[0][i] * inv;
+            } else {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) outv[db] = oacc[db][i] * inv;
+            }
+            *(typename VecN<DB>::T *)(orow + DB * r) = outv;
+        }
+        if (h32 == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
+    }
+}
+
+// Short sequences (S <= 64): HP heads per workgroup (2 or 4), each with 4/HP
+// waves of 32 queries, and key tiles of BC (64, or 32 when HP = 4); the
+// tiles of all HP heads sit side by side in LDS and are loaded through
+// registers (a sequence has one or two tiles, so there is nothing to
+// overlap the copies with).
+template <int D, bool CAUSAL, int HP, int BC>
+__global__ __launch_bounds__(kThreads, 1) void attn_fwd_packed(FwdArgs a)
+{
+    static_assert(HP == 2 || HP == 4, "one-head workgroups use attn_fwd_kernel");
     constexpr int DH = D / 2;   // contraction length per lane half (k-steps)
     constexpr int DB = D / 32;  // 32-row blocks of O^T
     constexpr int KSTR = D + 4; // padded K row: conflict-free column reads
@@ -69,19 +347,8 @@ __global__ __launch_bounds__(kThreads, HP == 1 ? (D == 64 ? 3 : 2) : 1) void att
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
 
-    // Heavy (late) query blocks first so the causal triangle load-balances.
-    int bh, qb, bh0;
-    if (HP == 1) {
-        const int BH = (int)(gridDim.x / a.nqb);
-        const int qbr = blockIdx.x / BH;
-        bh = blockIdx.x - qbr * BH;
-        qb = CAUSAL ? (a.nqb - 1 - qbr) : qbr;
-        bh0 = bh;
-    } else {
-        bh0 = blockIdx.x * HP;
-        bh = bh0 + w / QB;
-        qb = 0;
-    }
+    const int bh0 = blockIdx.x * HP;
+    int bh = bh0 + w / QB;
     // A wave past the last head computes on the last head's data and stores
     // nothing (it still takes part in every barrier).
     const bool head_ok = bh < a.nbh;
@@ -89,11 +356,10 @@ __global__ __launch_bounds__(kThreads, HP == 1 ? (D == 64 ? 3 : 2) : 1) void att
     const int b = bh / a.H;
     const int hh = bh - b * a.H;
     const int S = a.S;
-    const int q0 = qb * 32 * QB;
-    const int m0 = q0 + 32 * (w % QB);
+    const int m0 = 32 * (w % QB);
     const int mq = m0 + l32;
-    const float *__restrict__ kslab = Ks + (HP == 1 ? 0 : (w / QB) * kBc * KSTR);
-    const float *__restrict__ vslab = Vs + (HP == 1 ? 0 : (w / QB) * kBc * D);
+    const float *__restrict__ kslab = Ks + (w / QB) * kBc * KSTR;
+    const float *__restrict__ vslab = Vs + (w / QB) * kBc * D;
 
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const float *__restrict__ qp = a.q + in_base;
@@ -117,15 +383,14 @@ __global__ __launch_bounds__(kThreads, HP == 1 ? (D == 64 ? 3 : 2) : 1) void att
     float mrun = -INFINITY;  // reference max of s*c for query mq (see below)
     float lrun = 0.0f;       // this lane half's share of the running sum
 
-    const int kend = CAUSAL ? min(S, q0 + 32 * QB) : S;
+    const int kend = CAUSAL ? min(S, 32 * QB) : S;
     const int ntiles = (kend + kBc - 1) / kBc;
     constexpr int kLoads = HP * kBc * D / 4 / kThreads;
     constexpr int kRowsPerLoad = kThreads / (D / 4);
-    static_assert(HP == 1 || kBc % kRowsPerLoad == 0, "a load row block must lie in one head");
-    // Base of the head each tile row block belongs to (HP > 1: head bh0 + hp,
+    static_assert(kBc % kRowsPerLoad == 0, "a load row block must lie in one head");
+    // Base of the head each tile row block belongs to (head bh0 + hp,
     // clamped to the last head).
     auto head_base = [&](int hp) -> int64_t {
-        if (HP == 1) return in_base;
         int h = bh0 + hp;
         if (h >= a.nbh) h = a.nbh - 1;
         const int hb = h / a.H;
@@ -472,15 +737,17 @@ int launch_fwd(FwdArgs args, int64_t nbh)
     if (args.S <= 32) {
         args.nqb = 1;
         const int nblocks = (int)((nbh + 3) / 4);
-        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, 4, 32>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 4, 32>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
     } else if (args.S <= 64) {
         args.nqb = 1;
         const int nblocks = (int)((nbh + 1) / 2);
-        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, 2, 64>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 2, 64>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
     } else {
         args.nqb = (args.S + kBr - 1) / kBr;
         const int nblocks = args.nqb * (int)nbh;
-        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, 1, 64>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
     }
     return launch_ok("attn_fwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
 }

@@ -16,6 +16,22 @@ __device__ __forceinline__ void dma16(const float *src, float *lds)
     __builtin_amdgcn_global_load_lds((gvoid *)src, (lvoid *)lds, 16, 0, 0);
 }
 
+// The same copy in buffer form (buffer_load_dwordx4 ... lds): the base
+// address lives in a scalar buffer descriptor and each lane supplies a
+// 32-bit byte offset, so a copy needs one offset register and no per-lane
+// 64-bit address arithmetic.  The descriptor's range is the full 4 GiB
+// (no clamping); its format word is the raw-buffer setting for gfx9 parts.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rsrc(const float *base)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, -1, 0x00020000);
+}
+
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, unsigned byte_off, float *lds)
+{
+    typedef __attribute__((address_space(3))) void lvoid;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lvoid *)lds, 16, byte_off, 0, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
 // and lgkmcnt left at their maxima): at most N of this wave's vector-memory
 // operations, including LDS-bound copies, are still in flight.
