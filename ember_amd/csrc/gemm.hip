@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(GemmArgs g)
 // 16-byte aligned operands): 128 x 256 block of out per workgroup, 64 x 128
 // per wave as 2 x 4 accumulators, two workgroups per CU.
 //   * k is walked in slabs of 16, copied HBM -> LDS directly
-//     (global_load_lds_dwordx4, no registers) one slab ahead into the
+//     (buffer_load_dwordx4 ... lds, no registers) one slab ahead into the
 //     other of two buffers; one barrier per slab.
 //   * A slab, a stored n x k: 128 tile rows padded to 20 floats, so the A
 //     operand (one row per lane, 4 k per ds_read_b128) hits 16 different
@@ -303,18 +303,21 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
     const float *A = g.a + (int64_t)blockIdx.y * g.sa + (TA ? (int64_t)row0 : (int64_t)row0 * g.lda);
     const float *B = g.b + (int64_t)blockIdx.y * g.sb + (TB ? (int64_t)col0 * g.ldb : (int64_t)col0);
 
-    // Per-lane offsets of the 1 KiB copies this wave issues (copy t = w + 4s).
+    // Per-lane offsets of the 1 KiB copies this wave issues (copy
+    // t = w + NW*s): bytes for the buffer-form copies (below 2^32 because
+    // lda, ldb < 2^22, checked on the host), floats for b stored m x k,
+    // whose copies keep the flat-address form (measured 2 % faster there).
     constexpr int AS = (ACOP + NW - 1) / NW, BS = (BCOP + NW - 1) / NW;
     unsigned aoff[AS], boff[BS];
 #pragma unroll
     for (int s = 0; s < AS; ++s) {
         const int t = w + NW * s;
         if (TA) {  // copy t: k-rows 2t, 2t+1, 32 chunks each
-            aoff[s] = (unsigned)((2 * t + h32) * g.lda + 4 * l32);
+            aoff[s] = 4u * (unsigned)((2 * t + h32) * g.lda + 4 * l32);
         } else {   // row p / 5, chunk p % 5 (chunk 4 is row padding: re-read chunk 0)
             const int p = 64 * t + lane;
             const int r = p / (FASTR / 4), c = p - r * (FASTR / 4);
-            aoff[s] = (unsigned)(r * g.lda + 4 * (c < 4 ? c : 0));
+            aoff[s] = 4u * (unsigned)(r * g.lda + 4 * (c < 4 ? c : 0));
         }
     }
 #pragma unroll
@@ -325,19 +328,25 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
             const int r = p / (FASTR / 4), c = p - r * (FASTR / 4);
             boff[s] = (unsigned)(r * g.ldb + 4 * (c < 4 ? c : 0));
         } else {   // copy t: k-row t
-            boff[s] = (unsigned)(t * g.ldb + 4 * lane);
+            boff[s] = 4u * (unsigned)(t * g.ldb + 4 * lane);
         }
     }
 
     auto fetch = [&](int k0, float *__restrict__ as, float *__restrict__ bs) {
-        const float *Ak = TA ? A + (int64_t)k0 * g.lda : A + k0;
-        const float *Bk = TB ? B + k0 : B + (int64_t)k0 * g.ldb;
+        const __amdgpu_buffer_rsrc_t ra = dma_rsrc(TA ? A + (int64_t)k0 * g.lda : A + k0);
 #pragma unroll
         for (int s = 0; s < AS; ++s)
-            if (w + NW * s < ACOP) dma16(Ak + aoff[s], as + 256 * (w + NW * s));
+            if (w + NW * s < ACOP) dma16_buf(ra, aoff[s], as + 256 * (w + NW * s));
+        if constexpr (TB) {
 #pragma unroll
-        for (int s = 0; s < BS; ++s)
-            if (w + NW * s < BCOP) dma16(Bk + boff[s], bs + 256 * (w + NW * s));
+            for (int s = 0; s < BS; ++s)
+                if (w + NW * s < BCOP) dma16(B + k0 + boff[s], bs + 256 * (w + NW * s));
+        } else {
+            const __amdgpu_buffer_rsrc_t rb = dma_rsrc(B + (int64_t)k0 * g.ldb);
+#pragma unroll
+            for (int s = 0; s < BS; ++s)
+                if (w + NW * s < BCOP) dma16_buf(rb, boff[s], bs + 256 * (w + NW * s));
+        }
     };
 
     f32x16 acc[2][4];
@@ -553,8 +562,10 @@ int gemm_launch(const float *a, const float *b, float *out, int batch, int n, in
     if (batch > 65535) return record_error(EMBER_ERR_UNSUPPORTED, who);
     const bool vec = (k % 4 == 0) && (m % 4 == 0) && (n % 4 == 0 || !ta) &&
                      (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
-    // The fast kernel moves out, pre and residual as 16-byte vectors.
-    if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 &&
+    // The fast kernel moves out, pre and residual as 16-byte vectors, and
+    // addresses a tile's rows with 32-bit byte offsets (row pitch < 2^22).
+    if (vec && n % FM == 0 && m % FN == 0 && k % FK == 0 && k > 0 && g.lda < (1 << 22) &&
+        g.ldb < (1 << 22) &&
         (((uintptr_t)out | (uintptr_t)pre | (uintptr_t)residual) % 16) == 0) {
         g.tiles_n = n / FM;
         g.tiles_m = m / FN;
