@@ -32,7 +32,7 @@
 //     around the dS exchange instead of two separated phases.
 //
 // Pipelining and instruction economy.  The next query block's Q, dO, lse2
-// and delta are copied HBM -> LDS directly (gfx950 global_load_lds_dwordx4,
+// and delta are copied HBM -> LDS directly (gfx950 buffer_load_dwordx4 ... lds,
 // no registers) into the second of two buffers while the current block is
 // multiplied.  All LDS tiles use padded rows (Q/dO: D+4 floats, dS: 128+4;
 // K: rows of D with the second half of the keys shifted by 32 floats) rather
@@ -143,36 +143,63 @@ struct BwdBlock {
     int S, nq, n0w, w;
     int in_ss, out_ss;
     // Per copy slot s (copy t = w + 4s of a tile): this lane's chunk as a
-    // source offset within the block for q and dO (-1: padding or slack,
-    // never read) and its row.
-    int qoff[kMaxSlots], goff[kMaxSlots], row[kMaxSlots];
+    // byte offset within the block for q and dO (0 for padding or slack:
+    // the block's first chunk, never read).
+    unsigned qoff[kMaxSlots], goff[kMaxSlots];
     bool key_tail;
 };
 
+// This lane's chunk of copy t of a Q / dO tile (padded rows): its row, and
+// whether it holds data (not row padding or slack past the tile).
+template <int D>
+__device__ __forceinline__ void bwd_chunk(int t, int lane, int &r, int &c4, bool &real)
+{
+    typedef BwdLayout<D> L;
+    const int p = 64 * t + lane;
+    r = p / L::QROWCH;
+    c4 = p - r * L::QROWCH;
+    real = p < L::QCHUNKS && c4 < D / 4;
+}
+
 // Copies query block m0's Q and dO tiles (padded rows) and its lse2 / delta
-// into one set of buffers.  Copy t of a tile fills chunks 64t .. 64t+63; a
-// padding or slack chunk reads row m0's first chunk (valid memory, never
-// used).  Rows past the end re-read row S-1; their lse2 is +inf, so they
-// contribute exactly 0.
+// into one set of buffers (buffer-form copies: the block base in a scalar
+// descriptor, a 32-bit byte offset per lane).  Copy t of a tile fills chunks
+// 64t .. 64t+63; a padding or slack chunk reads row m0's first chunk (valid
+// memory, never used).  Rows past the end re-read row S-1; their lse2 is
+// +inf, so they contribute exactly 0.  On that (last) block the offsets are
+// recomputed from an opaque lane index, so that the compiler keeps no
+// second set live across the loop.
 template <int D>
 __device__ __forceinline__ void bwd_fetch(const BwdBlock &k, int m0, float *__restrict__ qn,
                                           float *__restrict__ gn, float *__restrict__ stn)
 {
     typedef BwdLayout<D> L;
-    const float *qb = k.qp + (int64_t)m0 * k.in_ss;
-    const float *gb = k.gp + (int64_t)m0 * k.out_ss;
+    const __amdgpu_buffer_rsrc_t rq = dma_rsrc(k.qp + (int64_t)m0 * k.in_ss);
+    const __amdgpu_buffer_rsrc_t rg = dma_rsrc(k.gp + (int64_t)m0 * k.out_ss);
     const int rmax = k.S - 1 - m0;  // rows beyond it are clamped to it
+    if (rmax >= kBq - 1) {
 #pragma unroll
-    for (int s = 0; s < L::SLOTS; ++s) {
-        const int t = k.w + kWaves * s;
-        if (t < L::QDMA) {
-            const int cl = k.row[s] > rmax ? rmax - k.row[s] : 0;
-            // Unsigned (non-negative) offsets from a wave-uniform base let the
-            // copy use scalar-base + 32-bit vector-offset addressing.
-            const unsigned qo = k.qoff[s] < 0 ? 0u : (unsigned)(k.qoff[s] + cl * k.in_ss);
-            const unsigned go = k.goff[s] < 0 ? 0u : (unsigned)(k.goff[s] + cl * k.out_ss);
-            dma16(qb + qo, qn + 256 * t);
-            dma16(gb + go, gn + 256 * t);
+        for (int s = 0; s < L::SLOTS; ++s) {
+            const int t = k.w + kWaves * s;
+            if (t < L::QDMA) {
+                dma16_buf(rq, k.qoff[s], qn + 256 * t);
+                dma16_buf(rg, k.goff[s], gn + 256 * t);
+            }
+        }
+    } else {
+        int ln = threadIdx.x & 63;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int s = 0; s < L::SLOTS; ++s) {
+            const int t = k.w + kWaves * s;
+            if (t < L::QDMA) {
+                int r, c4;
+                bool real;
+                bwd_chunk<D>(t, ln, r, c4, real);
+                r = min(r, rmax);
+                dma16_buf(rq, real ? 4u * (unsigned)(r * k.in_ss + 4 * c4) : 0u, qn + 256 * t);
+                dma16_buf(rg, real ? 4u * (unsigned)(r * k.out_ss + 4 * c4) : 0u, gn + 256 * t);
+            }
         }
     }
     if (k.w == 0) {
@@ -391,7 +418,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    // Wave index, made provably uniform for D < 128 (scalar copy branches
+    // and LDS bases); at D = 128 the kernel is short of scalar registers and
+    // the plain form measured faster (2 % non-causal).
+    const int w = D == 128 ? tid >> 6 : __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
 
@@ -420,13 +450,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     k.key_tail = k.n0w + kBkw > S;
 #pragma unroll
     for (int s = 0; s < kMaxSlots; ++s) {
-        const int p = 64 * (w + kWaves * s) + lane;
-        const int r = p / L::QROWCH;
-        const int c4 = p - r * L::QROWCH;
-        const bool real = p < L::QCHUNKS && c4 < D / 4;
-        k.qoff[s] = real ? r * k.in_ss + 4 * c4 : -1;
-        k.goff[s] = real ? r * k.out_ss + 4 * c4 : -1;
-        k.row[s] = real ? r : 0;
+        int r, c4;
+        bool real;
+        bwd_chunk<D>(w + kWaves * s, lane, r, c4, real);
+        k.qoff[s] = real ? 4u * (unsigned)(r * k.in_ss + 4 * c4) : 0u;
+        k.goff[s] = real ? 4u * (unsigned)(r * k.out_ss + 4 * c4) : 0u;
     }
 
     // Resident B operands: lane holds K[nl][h32*DH + kk] and V[nl][...].
