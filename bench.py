@@ -132,7 +132,7 @@ def _timed(ev, fn, reps):
 
 
 def decoder_step(B, S, d, H, steps):
-    """Times config 5's training step; flops as SURVEY 8(d): 3 x the forward
+    """Times config 5's training step; flops: 3 x the forward
     GEMMs (2*B*S*d*d*(3 + 1 + 4 + 4)) plus causal attention fwd+bwd."""
     from ember_amd import Tensor, loss, nn, optim, random as erand
 
@@ -168,7 +168,7 @@ def decoder_step(B, S, d, H, steps):
 
 
 def secondary(L, ev):
-    """The other BASELINE configs, measured the same way (reported beside the
+    """The other benchmark configurations, measured the same way (reported beside the
     headline, not part of `value`): attention fwd at configs 1 and 2, the
     attention part of config 5 (fwd+bwd), the config-4 GEMM shapes, and the
     forward at short S where it is HBM-bound (achieved GB/s)."""

@@ -1,7 +1,7 @@
 // layernorm.hip -- LayerNorm forward / backward over the last dimension.
 //
-// No reference counterpart: Ember has no LayerNorm (SURVEY: config 5's
-// pre-LN decoder block composes it from sum_axis / broadcast / sqrt).  The
+// No reference counterpart: Ember has no LayerNorm (a pre-LN decoder
+// block built from Ember ops composes it from sum_axis / broadcast / sqrt).  The
 // semantics are those of oracle/ember_oracle.c (oracle_layernorm_*):
 //   mean = sum(x)/d;  var = sum((x - mean)^2)/d  (biased);
 //   rstd = 1/sqrt(var + eps);  y = (x - mean)*rstd*gamma + beta
