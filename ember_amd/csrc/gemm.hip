@@ -291,8 +291,11 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
     const int first = grp * GROUP;
     const int rows_in_grp = min(GROUP, g.tiles_n - first);
     const int in_grp = tile - grp * per_group;
-    const int row0 = (first + in_grp % rows_in_grp) * TM;
-    const int col0 = (in_grp / rows_in_grp) * FN;
+    // The tile origin is computed with vector integer division; made
+    // provably uniform here, it stays in scalar registers and the buffer
+    // descriptors built from it need no per-lane (waterfall) handling.
+    const int row0 = __builtin_amdgcn_readfirstlane((first + in_grp % rows_in_grp) * TM);
+    const int col0 = __builtin_amdgcn_readfirstlane((in_grp / rows_in_grp) * FN);
 
     int kbeg = 0, kend = g.k;
     if (SPLIT) {
@@ -303,10 +306,8 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
     const float *A = g.a + (int64_t)blockIdx.y * g.sa + (TA ? (int64_t)row0 : (int64_t)row0 * g.lda);
     const float *B = g.b + (int64_t)blockIdx.y * g.sb + (TB ? (int64_t)col0 * g.ldb : (int64_t)col0);
 
-    // Per-lane offsets of the 1 KiB copies this wave issues (copy
-    // t = w + NW*s): bytes for the buffer-form copies (below 2^32 because
-    // lda, ldb < 2^22, checked on the host), floats for b stored m x k,
-    // whose copies keep the flat-address form (measured 2 % faster there).
+    // Per-lane byte offsets of the 1 KiB copies this wave issues (copy
+    // t = w + NW*s), below 2^32 because lda, ldb < 2^22 (checked on the host).
     constexpr int AS = (ACOP + NW - 1) / NW, BS = (BCOP + NW - 1) / NW;
     unsigned aoff[AS], boff[BS];
 #pragma unroll
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
         if (TB) {
             const int p = 64 * t + lane;
             const int r = p / (FASTR / 4), c = p - r * (FASTR / 4);
-            boff[s] = (unsigned)(r * g.ldb + 4 * (c < 4 ? c : 0));
+            boff[s] = 4u * (unsigned)(r * g.ldb + 4 * (c < 4 ? c : 0));
         } else {   // copy t: k-row t
             boff[s] = 4u * (unsigned)(t * g.ldb + 4 * lane);
         }
@@ -337,16 +338,10 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
 #pragma unroll
         for (int s = 0; s < AS; ++s)
             if (w + NW * s < ACOP) dma16_buf(ra, aoff[s], as + 256 * (w + NW * s));
-        if constexpr (TB) {
+        const __amdgpu_buffer_rsrc_t rb = dma_rsrc(TB ? B + k0 : B + (int64_t)k0 * g.ldb);
 #pragma unroll
-            for (int s = 0; s < BS; ++s)
-                if (w + NW * s < BCOP) dma16(B + k0 + boff[s], bs + 256 * (w + NW * s));
-        } else {
-            const __amdgpu_buffer_rsrc_t rb = dma_rsrc(B + (int64_t)k0 * g.ldb);
-#pragma unroll
-            for (int s = 0; s < BS; ++s)
-                if (w + NW * s < BCOP) dma16_buf(rb, boff[s], bs + 256 * (w + NW * s));
-        }
+        for (int s = 0; s < BS; ++s)
+            if (w + NW * s < BCOP) dma16_buf(rb, boff[s], bs + 256 * (w + NW * s));
     };
 
     f32x16 acc[2][4];
