@@ -78,6 +78,62 @@ def attention_flops(B, H, S, D, causal=True):
     return fwd, 2.5 * fwd
 
 
+def _run_threads(fn, items):
+    """Wall seconds of fn(item) for every item, one host thread each (the
+    C calls release the GIL)."""
+    ts = [threading.Thread(target=fn, args=(it,)) for it in items]
+    t0 = time.perf_counter()
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    return time.perf_counter() - t0
+
+
+def cpu_other_configs(threads):
+    """The reference's CPU operators on bounded samples of configs 1, 2 and 4
+    (reported beside the GPU figures of the same configs, not targets):
+    config 1 in full (its 4 heads, one per thread), `threads` heads of
+    config 2's shape (causal forward, one per thread), and `threads`
+    independent 1024^3 matmuls (the reference's FP64-accumulating loop)."""
+    import oracle
+
+    if not oracle.ref_available():
+        return None
+    R = oracle.ref_lib()
+    rng = np.random.default_rng(4321)
+    out = {}
+
+    def attn_fwd(S, D, causal, nheads):
+        heads = [tuple(rng.standard_normal((S, D)).astype(np.float32) for _ in range(3))
+                 for _ in range(nheads)]
+        scale = oracle.default_scale(D)
+        wall = _run_threads(lambda h: oracle.ref_composed_attention_head(h[0], h[1], h[2], None, causal,
+                                                                         scale, backward=False), heads)
+        fwd, _ = attention_flops(1, nheads, S, D, causal)
+        return wall, fwd
+
+    wall, fl = attn_fwd(256, 64, False, 4)
+    out["config1_fwd"] = {"value": fl / wall / 1e12, "unit": "TFLOP/s", "cores": 4, "wall_s": wall,
+                          "sample": "config 1 in full: B1 H4 S256 D64 non-causal fwd, one head per thread"}
+    wall, fl = attn_fwd(2048, 64, True, threads)
+    out["config2_causal_fwd"] = {"value": fl / wall / 1e12, "unit": "TFLOP/s", "cores": threads, "wall_s": wall,
+                                 "sample": f"{threads} of config 2's 128 heads (S2048 D64 causal fwd), one per thread"}
+    n = 1024
+    mats = [(rng.uniform(-1, 1, (n, n)).astype(np.float32), rng.uniform(-1, 1, (n, n)).astype(np.float32))
+            for _ in range(threads)]
+
+    def mm(ab):
+        c = np.empty((n, n), dtype=np.float32)
+        R.matmul(ab[0], ab[1], c, n, n, n)
+
+    wall = _run_threads(mm, mats)
+    out["config4_gemm_1024"] = {"value": 2.0 * n ** 3 * threads / wall / 1e12, "unit": "TFLOP/s", "cores": threads,
+                                "wall_s": wall,
+                                "sample": f"{threads} independent 1024^3 matmuls with operators_cpu.c's matmul, one per thread"}
+    return out
+
+
 def cpu_baseline(S, D, threads):
     """Times Ember's CPU path on `threads` heads (one per thread), fwd+bwd."""
     import oracle
@@ -97,13 +153,7 @@ def cpu_baseline(S, D, threads):
             oracle.attention_bwd(q[None, None], k[None, None], v[None, None], o, lse,
                                  d_o[None, None], True, scale)
 
-    ts = [threading.Thread(target=run, args=(h,)) for h in heads]
-    t0 = time.perf_counter()
-    for t in ts:
-        t.start()
-    for t in ts:
-        t.join()
-    wall = time.perf_counter() - t0
+    wall = _run_threads(run, heads)
     fwd, bwd = attention_flops(1, threads, S, D)
     what = ("the reference's operators_cpu.c ops composed as Ember would (matmul, transpose, "
             "mul_scalar, add_tensor mask, softmax via max_axis/sub/exp/sum_axis/div; "
@@ -429,6 +479,9 @@ def main(argv=None):
         threads = min(16, os.cpu_count() or 1)
     if threads > 0:
         result["cpu_baseline"] = cpu_baseline(S, D, threads)
+        others = cpu_other_configs(threads)
+        if others is not None:
+            result["cpu_baseline"]["other_configs"] = others
     print(json.dumps(result), flush=True)
     return 0
 
