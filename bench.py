@@ -13,9 +13,12 @@ which is the stream every kernel of the library is launched on.
 
 The CPU baseline runs Ember's own CPU operators (the reference's
 operators_cpu.c, compiled in place under oracle/_ref) composed the way Ember
-expresses attention today, on a bounded sample: one full-size head
-(S=4096, D=128) per host thread, fwd+bwd.  It falls back to this
-repository's C restatement (oracle/ember_oracle.c) when _ref is absent.
+expresses attention today, on a bounded sample of the timed workload itself:
+heads 0..15 of batch 0 (S=4096, D=128), one per host thread, fwd+bwd.  It
+falls back to this repository's C restatement (oracle/ember_oracle.c) when
+_ref is absent.  The same leg times the reference on samples of configs 1, 2
+and 4, and compares every CPU result with the GPU's output for the same
+inputs (`parity_vs_gpu`: max error and max error / (2e-4 + 1e-3 |ref|)).
 """
 
 from __future__ import annotations
@@ -90,68 +93,100 @@ def _run_threads(fn, items):
     return time.perf_counter() - t0
 
 
-def cpu_other_configs(threads):
-    """The reference's CPU operators on bounded samples of configs 1, 2 and 4
-    (reported beside the GPU figures of the same configs, not targets):
-    config 1 in full (its 4 heads, one per thread), `threads` heads of
-    config 2's shape (causal forward, one per thread), and `threads`
-    independent 1024^3 matmuls (the reference's FP64-accumulating loop)."""
+ATOL, RTOL = 2e-4, 1e-3  # the parity tolerance for O, dQ, dK, dV (and the GEMM)
+
+
+def _parity(pairs):
+    """max |gpu - ref| and max |gpu - ref| / (ATOL + RTOL |ref|) over (gpu, ref) pairs."""
+    err = ratio = 0.0
+    for g, r in pairs:
+        d = np.abs(g.astype(np.float64) - r.astype(np.float64))
+        err = max(err, float(d.max()))
+        ratio = max(ratio, float((d / (ATOL + RTOL * np.abs(r.astype(np.float64)))).max()))
+    return {"max_abs_err": err, "max_err_over_tol": ratio, "within_tolerance": ratio <= 1.0}
+
+
+def cpu_other_configs(threads, keep):
+    """The reference's CPU operators on bounded samples of configs 1, 2 and 4,
+    on the very inputs the GPU ran in `secondary`, timed (reported beside the
+    GPU figures, not targets) and compared with the GPU outputs: config 1 in
+    full (its 4 heads, one per thread), `threads` heads of config 2 (causal
+    forward, one per thread), and `threads` blocks of 8 rows of config 4's
+    4096^3 product (the reference's FP64-accumulating matmul, one block per
+    thread)."""
     import oracle
 
-    if not oracle.ref_available():
+    if not oracle.ref_available() or keep is None:
         return None
     R = oracle.ref_lib()
-    rng = np.random.default_rng(4321)
     out = {}
 
-    def attn_fwd(S, D, causal, nheads):
-        heads = [tuple(rng.standard_normal((S, D)).astype(np.float32) for _ in range(3))
-                 for _ in range(nheads)]
+    def attn_fwd(tag, q, k, v, o_gpu, causal, heads, sample):
+        S, D = q.shape[2:]
         scale = oracle.default_scale(D)
-        wall = _run_threads(lambda h: oracle.ref_composed_attention_head(h[0], h[1], h[2], None, causal,
-                                                                         scale, backward=False), heads)
-        fwd, _ = attention_flops(1, nheads, S, D, causal)
-        return wall, fwd
+        res = {}
 
-    wall, fl = attn_fwd(256, 64, False, 4)
-    out["config1_fwd"] = {"value": fl / wall / 1e12, "unit": "TFLOP/s", "cores": 4, "wall_s": wall,
-                          "sample": "config 1 in full: B1 H4 S256 D64 non-causal fwd, one head per thread"}
-    wall, fl = attn_fwd(2048, 64, True, threads)
-    out["config2_causal_fwd"] = {"value": fl / wall / 1e12, "unit": "TFLOP/s", "cores": threads, "wall_s": wall,
-                                 "sample": f"{threads} of config 2's 128 heads (S2048 D64 causal fwd), one per thread"}
-    n = 1024
-    mats = [(rng.uniform(-1, 1, (n, n)).astype(np.float32), rng.uniform(-1, 1, (n, n)).astype(np.float32))
-            for _ in range(threads)]
+        def one(bh):
+            b, h = bh
+            res[bh] = oracle.ref_composed_attention_head(q[b, h], k[b, h], v[b, h], None, causal, scale,
+                                                         backward=False)[0]
 
-    def mm(ab):
-        c = np.empty((n, n), dtype=np.float32)
-        R.matmul(ab[0], ab[1], c, n, n, n)
+        wall = _run_threads(one, heads)
+        fwd, _ = attention_flops(1, len(heads), S, D, causal)
+        out[tag] = {"value": fwd / wall / 1e12, "unit": "TFLOP/s", "cores": len(heads), "wall_s": wall,
+                    "sample": sample,
+                    "parity_vs_gpu": _parity([(o_gpu[b, h], res[(b, h)]) for (b, h) in heads])}
 
-    wall = _run_threads(mm, mats)
-    out["config4_gemm_1024"] = {"value": 2.0 * n ** 3 * threads / wall / 1e12, "unit": "TFLOP/s", "cores": threads,
-                                "wall_s": wall,
-                                "sample": f"{threads} independent 1024^3 matmuls with operators_cpu.c's matmul, one per thread"}
+    q, k, v, o = keep["config1_fwd"]
+    attn_fwd("config1_fwd", q, k, v, o, False, [(0, h) for h in range(4)],
+             "config 1 in full: B1 H4 S256 D64 non-causal fwd, one head per thread")
+    q, k, v, o = keep["config2_causal_fwd"]
+    B, H = q.shape[:2]
+    heads = [(i % B, (7 * i) % H) for i in range(threads)]
+    attn_fwd("config2_causal_fwd", q, k, v, o, True, heads,
+             f"{threads} of config 2's {B * H} heads (S2048 D64 causal fwd), one per thread")
+
+    a, b, c = keep["config4_gemm_4096"]
+    n, kk = a.shape
+    m = b.shape[1]
+    blocks = [tuple(range(i * (n // threads), i * (n // threads) + 8)) for i in range(threads)]
+    res = {}
+
+    def mm(rs):
+        blk = np.ascontiguousarray(a[list(rs)])
+        r = np.empty((len(rs), m), dtype=np.float32)
+        R.matmul(blk, b, r, len(rs), m, kk)
+        res[rs] = r
+
+    wall = _run_threads(mm, blocks)
+    out["config4_gemm_4096"] = {
+        "value": 2.0 * 8 * threads * m * kk / wall / 1e12, "unit": "TFLOP/s", "cores": threads, "wall_s": wall,
+        "sample": f"{threads} blocks of 8 rows of the 4096^3 product with operators_cpu.c's matmul, one per thread",
+        "parity_vs_gpu": _parity([(c[list(rs)], res[rs]) for rs in blocks])}
     return out
 
 
-def cpu_baseline(S, D, threads):
-    """Times Ember's CPU path on `threads` heads (one per thread), fwd+bwd."""
+def cpu_baseline(S, D, threads, inputs, outputs):
+    """Times Ember's CPU path on `threads` heads of the timed workload (batch
+    0, heads 0..threads-1, one per thread), fwd+bwd, and compares its
+    O, dQ, dK, dV with the GPU's for the same heads."""
     import oracle
 
-    rng = np.random.default_rng(1234)
-    heads = [tuple(rng.standard_normal((S, D)).astype(np.float32) for _ in range(4))
-             for _ in range(threads)]
+    q, k, v, d_o = inputs
+    heads = list(range(threads))
     scale = oracle.default_scale(D)
     kind = "reference" if oracle.ref_available() else "port"
+    res = {}
 
     def run(h):
-        q, k, v, d_o = h
         if kind == "reference":
-            oracle.ref_composed_attention_head(q, k, v, d_o, True, scale, backward=True)
+            res[h] = oracle.ref_composed_attention_head(q[0, h], k[0, h], v[0, h], d_o[0, h], True, scale,
+                                                        backward=True)
         else:
-            o, lse = oracle.attention_fwd(q[None, None], k[None, None], v[None, None], True, scale)
-            oracle.attention_bwd(q[None, None], k[None, None], v[None, None], o, lse,
-                                 d_o[None, None], True, scale)
+            sl = (slice(0, 1), slice(h, h + 1))
+            o, lse = oracle.attention_fwd(q[sl], k[sl], v[sl], True, scale)
+            dq, dk, dv = oracle.attention_bwd(q[sl], k[sl], v[sl], o, lse, d_o[sl], True, scale)
+            res[h] = (o[0, 0], dq[0, 0], dk[0, 0], dv[0, 0])
 
     wall = _run_threads(run, heads)
     fwd, bwd = attention_flops(1, threads, S, D)
@@ -164,9 +199,11 @@ def cpu_baseline(S, D, threads):
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": kind,
-        "sample": f"{threads} head(s) of S={S} D={D} causal fwd+bwd, one per thread, "
-                  f"{wall:.1f} s wall; {what}; flops counted as on the GPU (causal half)",
+        "sample": f"{threads} head(s) of the timed workload (batch 0, heads 0..{threads - 1}; S={S} D={D} "
+                  f"causal fwd+bwd), one per thread, {wall:.1f} s wall; {what}; flops counted as on the GPU "
+                  f"(causal half)",
         "wall_s": wall,
+        "parity_vs_gpu": _parity([(g[0, h], r) for h in heads for g, r in zip(outputs, res[h])]),
     }
 
 
@@ -222,14 +259,14 @@ def secondary(L, ev):
     headline, not part of `value`): attention fwd at configs 1 and 2, the
     attention part of config 5 (fwd+bwd), the config-4 GEMM shapes, and the
     forward at short S where it is HBM-bound (achieved GB/s)."""
-    out = {}
+    out, keep = {}, {}
     rng = np.random.default_rng(5)
 
-    def attn(tag, B, H, S, D, causal, bwd, reps):
+    def attn(tag, B, H, S, D, causal, bwd, reps, kept=False):
         n = B * H * S * D
-        host = rng.standard_normal(n, dtype=np.float32)
-        q, k, v = (DeviceArray((n,), host) for _ in range(3))
-        g = DeviceArray((n,), host) if bwd else None
+        hosts = [rng.standard_normal(n, dtype=np.float32) for _ in range(3)]
+        q, k, v = (DeviceArray((n,), h) for h in hosts)
+        g = DeviceArray((n,), hosts[0]) if bwd else None
         o, lse = DeviceArray((n,)), DeviceArray((B * H * S,))
         dq, dk, dv = (DeviceArray((n,)) for _ in range(3)) if bwd else (None, None, None)
         st = capi.contiguous_strides(B, H, S, D)
@@ -250,9 +287,11 @@ def secondary(L, ev):
         rec["fwd_hbm_gbs"] = round(fwd_bytes / fwd_ms / 1e6, 1)
         capi.check(what=tag)
         out[tag] = rec
+        if kept:  # inputs and output, for the CPU leg's comparison
+            keep[tag] = tuple(x.reshape(B, H, S, D) for x in hosts + [o.numpy()])
 
-    attn("config1_fwd", 1, 4, 256, 64, False, False, 50)
-    attn("config2_causal_fwd", 8, 16, 2048, 64, True, False, 20)
+    attn("config1_fwd", 1, 4, 256, 64, False, False, 50, kept=True)
+    attn("config2_causal_fwd", 8, 16, 2048, 64, True, False, 20, kept=True)
     attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20)
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
@@ -322,15 +361,18 @@ def secondary(L, ev):
 
     for tag, (n, k, m) in {"config4_gemm_4096": (4096, 4096, 4096),
                            "config4_gemm_16384x1024x3072": (16384, 1024, 3072)}.items():
-        a = DeviceArray((n * k,), rng.uniform(-1, 1, n * k).astype(np.float32))
-        b = DeviceArray((k * m,), rng.uniform(-1, 1, k * m).astype(np.float32))
+        a_h = rng.uniform(-1, 1, n * k).astype(np.float32)
+        b_h = rng.uniform(-1, 1, k * m).astype(np.float32)
+        a, b = DeviceArray((n * k,), a_h), DeviceArray((k * m,), b_h)
         c = DeviceArray((n * m,))
         ms = _timed(ev, lambda: L.matmul(a.ptr, b.ptr, c.ptr, n, m, k), 10)
         capi.check(what=tag)
+        if tag == "config4_gemm_4096":
+            keep[tag] = (a_h.reshape(n, k), b_h.reshape(k, m), c.numpy().reshape(n, m))
         out[tag] = {"shape": f"n={n} k={k} m={m}", "ms": round(ms, 4),
                     "tflops": round(2.0 * n * m * k / ms / 1e9, 2),
                     "frac_of_fp32_mfma_peak": round(2.0 * n * m * k / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS, 4)}
-    return out
+    return out, keep
 
 
 def main(argv=None):
@@ -373,7 +415,6 @@ def main(argv=None):
     rng = np.random.default_rng(0)
     host = [rng.standard_normal((B, H, S, D), dtype=np.float32) for _ in range(4)]
     q, k, v, d_o = (DeviceArray.from_numpy(x) for x in host)
-    del host
     o = DeviceArray((B, H, S, D))
     lse = DeviceArray((B, H, S))
     dq, dk, dv = (DeviceArray((B, H, S, D)) for _ in range(3))
@@ -471,15 +512,18 @@ def main(argv=None):
         capi.check(what="copy probe")
         result["copy_probe_bytes"] = {"read": 4 * n, "write": 4 * n}
 
+    keep = None
     if not args.no_secondary:
-        result["secondary"] = secondary(L, ev)
+        result["secondary"], keep = secondary(L, ev)
 
     threads = args.cpu_threads
     if threads is None:
         threads = min(16, os.cpu_count() or 1)
     if threads > 0:
-        result["cpu_baseline"] = cpu_baseline(S, D, threads)
-        others = cpu_other_configs(threads)
+        cpu_heads = min(threads, H)
+        gpu_out = [x.numpy()[:1, :cpu_heads] for x in (o, dq, dk, dv)]
+        result["cpu_baseline"] = cpu_baseline(S, D, cpu_heads, [x[:1, :cpu_heads] for x in host], gpu_out)
+        others = cpu_other_configs(threads, keep)
         if others is not None:
             result["cpu_baseline"]["other_configs"] = others
     print(json.dumps(result), flush=True)
