@@ -11,10 +11,11 @@
 // directly (buffer_load_dwordx4 ... lds, no registers) and overlap the
 // products: V of tile t lands while S of tile t is computed, K of tile t+1
 // while V of tile t is multiplied; two barriers per tile.
-// Short sequences pack heads instead (attn_fwd_packed): S <= 32 puts 4
-// heads in a workgroup (one per wave, tiles of 32 keys) and S <= 64 puts 2
-// (two waves each), so that no wave idles and the HBM-bound forward keeps
-// every wave loading.
+// Short sequences (S <= 64, HBM-bound) use one wave per 32-query block
+// instead, with no barriers (attn_fwd_wave, D = 128), or pack heads
+// (attn_fwd_packed, D <= 64): S <= 32 puts 4 heads in a workgroup (one per
+// wave, tiles of 32 keys) and S <= 64 puts 2 (two waves each), so that no
+// wave idles and every wave keeps loading.
 //
 // Per tile and wave (all products on v_mfma_f32_32x32x2f32):
 //   S^T (64 keys x 32 queries) = K_tile . Q^T   -- K from LDS, Q^T resident in
@@ -319,6 +320,161 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
                 for (int db = 0; db < DB; ++db) outv[db] = oacc[db][i] * inv;
             }
             *(typename VecN<DB>::T *)(orow + DB * r) = outv;
+        }
+        if (h32 == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
+    }
+}
+
+// D = 128, S <= 64: one wave per (head, 32-query block), four independent
+// waves per workgroup (consecutive query blocks of a head share one) and no
+// barriers, so that two waves per SIMD overlap one's copies with another's
+// products in this HBM-bound regime.  Each wave stages its Q tile, then
+// each 32-key K tile, through a private padded LDS slice with coalesced
+// copies (buffer_load ... lds: an MFMA operand puts one row per lane, which
+// read straight from HBM would touch 64 lines per load), and loads V
+// straight into registers in operand order (already row-contiguous across
+// lanes).  Per tile: S^T = K.Q^T, the online softmax of attn_fwd_kernel,
+// O^T += V^T.P^T.  Rows past the sequence end re-read row S-1 (masked).
+template <int D>
+struct WaveSlice {
+    static constexpr int STR = D + 4;                // padded row (floats)
+    static constexpr int CH = STR / 4;               // 16-byte chunks per row
+    static constexpr int COP = (32 * CH + 63) / 64;  // 1 KiB copies per 32-row tile
+    static constexpr int BUF = COP * 256;            // floats per wave slice
+};
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
+{
+    typedef WaveSlice<D> T;
+    constexpr int DH = D / 2;
+    constexpr int DB = D / 32;
+    typedef typename VecN<DB>::T VT;
+    __shared__ float slab[kWaves * T::BUF];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    float *__restrict__ buf = slab + w * T::BUF;
+
+    const int item = blockIdx.x * kWaves + w;  // query block fastest
+    if (item >= a.nbh * a.nqb) return;         // no barriers below: safe to leave
+    const int bh = item / a.nqb;
+    const int qb = item - bh * a.nqb;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int m0 = 32 * qb;
+    const int mq = m0 + l32;
+    const int in_ss = (int)a.in_ss;  // < 2^24 (checked on the host)
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const float *__restrict__ vb = a.v + in_base;
+
+    // Copies rows r0 .. r0+31 (clamped to S-1) of a (S, D) slab into buf;
+    // copy t fills chunks 64t .. 64t+63, a padding or slack chunk re-reads
+    // the first chunk.  Offsets are recomputed per call from an opaque lane
+    // index, so that they do not stay live in registers.
+    auto stage = [&](const float *base, int r0) {
+        const __amdgpu_buffer_rsrc_t rs = dma_rsrc(base + (int64_t)r0 * in_ss);
+        const int rmax = S - 1 - r0;
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int t = 0; t < T::COP; ++t) {
+            const int p = 64 * t + ln;
+            const int r = p / T::CH, c = p - r * T::CH;
+            const unsigned off = c < D / 4 ? 4u * (unsigned)(min(r, rmax) * in_ss + 4 * c) : 0u;
+            dma16_buf(rs, off, buf + 256 * t);
+        }
+    };
+
+    // Q^T operand: lane holds Q[mq][h32*DH + kk] for k-step kk.
+    stage(a.q + in_base, m0);
+    wait_vmem();
+    float qr[DH];
+#pragma unroll
+    for (int kk = 0; kk < DH; kk += 4) {
+        const f32x4 t = *(const f32x4 *)&buf[l32 * T::STR + h32 * DH + kk];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qr[kk + j] = t[j];
+    }
+
+    f32x16 oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = zero16();
+    float mrun = -INFINITY, lrun = 0.0f;
+
+    const int kend = CAUSAL ? min(S, m0 + 32) : S;
+    for (int n0 = 0; n0 < kend; n0 += 32) {
+        wait_lds();  // this wave's earlier reads of buf are complete before the copy overwrites it
+        stage(a.k + in_base, n0);
+        VT vr[16];   // V operand for k-step i: V[n0 + acc_row(i, h32)][DB*l32 .. +DB)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int nv = n0 + acc_row(i, h32);
+            nv = nv < S ? nv : S - 1;
+            vr[i] = *(const VT *)(vb + (int64_t)nv * a.in_ss + DB * l32);
+        }
+        wait_vmem();
+        f32x16 sacc = zero16();
+#pragma unroll
+        for (int kk = 0; kk < DH; kk += 4) {
+            const f32x4 kf = *(const f32x4 *)&buf[l32 * T::STR + h32 * DH + kk];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sacc = mfma_32x32x2(kf[j], qr[kk + j], sacc);
+        }
+        const bool need_mask = n0 + 32 > S || (CAUSAL && n0 + 31 > m0);
+        if (need_mask) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int n = n0 + acc_row(i, h32);
+                const bool vis = (n < S) & (!CAUSAL | (n <= mq));
+                sacc[i] = vis ? sacc[i] : -INFINITY;
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sacc[i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        // Lazy rescaling as in attn_fwd_kernel; tile 0 holds key 0, visible
+        // to every query, so it sets a finite mrun.
+        const float tm2 = tmax * a.c;
+        if (__ballot(tm2 > mrun + 8.0f) != 0) {
+            const float mnew = fmaxf(mrun, tm2);
+            const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+            mrun = mnew;
+            lrun *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float sv = sacc[i];
+            const float p = need_mask && sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv, a.c, -mrun));
+            sacc[i] = p;
+            lrun += p;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) oacc[db] = mfma_32x32x2(vget<DB>(vr[i], db), sacc[i], oacc[db]);
+    }
+
+    const float ltot = lrun + __shfl_xor(lrun, 32);
+    if (mq < S) {
+        const float inv = 1.0f / ltot;
+        float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = acc_row(i, h32);  // O^T row block index -> d = DB*r + db
+            VT outv;
+            if constexpr (DB == 1) {
+                outv = oacc[0][i] * inv;
+            } else {
+#pragma unroll
+                for (int db = 0; db < DB; ++db) outv[db] = oacc[db][i] * inv;
+            }
+            *(VT *)(orow + DB * r) = outv;
         }
         if (h32 == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
     }
@@ -733,6 +889,18 @@ int launch_fwd(FwdArgs args, int64_t nbh)
         hipLaunchKernelGGL((attn_fwd_split<D, CAUSAL>), dim3((unsigned)(args.nqb * nbh)), dim3(kThreads),
                            0, 0, args);
         return launch_ok("attn_fwd_split") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
+    if constexpr (D == 128) {
+        // Measured: the wave kernel moves 4.7 (S = 32) and 4.0 TB/s (S = 64)
+        // where the packed kernel moves 3.8 and 2.9; at D <= 64 the packed
+        // kernel is as fast or faster.
+        if (args.S <= 64) {
+            args.nqb = (args.S + 31) / 32;
+            const int64_t items = (int64_t)args.nqb * nbh;
+            hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
+                               dim3(kThreads), 0, 0, args);
+            return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
+        }
     }
     if (args.S <= 32) {
         args.nqb = 1;

@@ -47,4 +47,10 @@ __device__ __forceinline__ void wait_vmem()
     wait_vmem_n<0>();
 }
 
+// s_waitcnt lgkmcnt(0): this wave's LDS reads (and scalar loads) are done.
+__device__ __forceinline__ void wait_lds()
+{
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
 }  // namespace ember

@@ -146,13 +146,12 @@ def test_config3_causal_fwd_bwd_slice():
 # ------------------------------------------------------- bitwise invariants
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_causal_mask_does_not_leak(D):
+@pytest.mark.parametrize("S,D", [(300, 64), (300, 128), (64, 128), (40, 64)])
+def test_causal_mask_does_not_leak(S, D):
     """Changing keys/values after row i leaves O and LSE of rows <= i bitwise unchanged."""
-    S = 300
     q, k, v, _ = _inputs(1, 1, S, D, seed=400 + D)
     o, lse = G.attention_fwd(q, k, v, True)
-    for i in (0, 63, 64, 127, 128, 200):
+    for i in (x for x in (0, 31, 32, 63, 64, 127, 128, 200) if x < S - 1):
         k2, v2 = k.copy(), v.copy()
         k2[0, 0, i + 1:] = _rand((S - i - 1, D), i)
         v2[0, 0, i + 1:] = _rand((S - i - 1, D), i + 1)
@@ -199,12 +198,14 @@ def test_backward_last_key_sees_only_last_query():
 # ------------------------------------------------------------ strided layout
 
 
-def test_packed_qkv_layout():
-    """q, k, v read from one (B, S, 3, H, D) buffer; o / dO in (B, S, H, D)."""
+@pytest.mark.parametrize("S,D", [(160, 64), (48, 128), (300, 128)])
+def test_packed_qkv_layout(S, D):
+    """q, k, v read from one (B, S, 3, H, D) buffer; o / dO in (B, S, H, D)
+    (S = 48, D = 128 takes the one-wave-per-query-block forward)."""
     from ember_amd import capi
     from ember_amd.capi import DeviceArray
 
-    B, H, S, D = 2, 4, 160, 64
+    B, H = 2, 4
     qkv = _rand((B, S, 3, H, D), 900)
     d_o_bshd = _rand((B, S, H, D), 901)
     q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
