@@ -356,6 +356,20 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
     // P[m][n] = 0 where t > 8(i/4) + i%4 (see the mask note above).
     const int t = (CAUSAL ? k.n0w + l32 - m0 - 4 * h32 : -1) + tail_bias;
     dq_softmax<D, PREV, MASK>(a, ds, kall, dqs, l2v, dlv, t, sacc, pacc, qacc);
+    // D < 128: P and dS are pinned here (an empty asm that reads and writes
+    // them), so that the compiler computes them interleaved with the dQ
+    // MFMAs above instead of sinking them past the dQ store's branches into
+    // the dV/dK block, where nothing hides them (measured +3.7 % at D = 64;
+    // at D = 128 the sunk form is 0.8 % faster).
+    if constexpr (D < 128) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float x = sacc[i], y = pacc[i];
+            asm volatile("" : "+v"(x), "+v"(y));
+            sacc[i] = x;
+            pacc[i] = y;
+        }
+    }
     if (PREV) dq_store<D>(a, k, m0 - kBq, qacc);
 
     // ---- dV += P^T dO, dK += dS^T Q ----
