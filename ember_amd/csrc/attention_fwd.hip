@@ -890,34 +890,31 @@ int launch_fwd(FwdArgs args, int64_t nbh)
                            0, 0, args);
         return launch_ok("attn_fwd_split") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
+    if (args.S > 64) {
+        args.nqb = (args.S + kBr - 1) / kBr;
+        const int nblocks = args.nqb * (int)nbh;
+        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
     if constexpr (D == 128) {
         // Measured: the wave kernel moves 4.7 (S = 32) and 4.0 TB/s (S = 64)
         // where the packed kernel moves 3.8 and 2.9; at D <= 64 the packed
         // kernel is as fast or faster.
-        if (args.S <= 64) {
-            args.nqb = (args.S + 31) / 32;
-            const int64_t items = (int64_t)args.nqb * nbh;
-            hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
-                               dim3(kThreads), 0, 0, args);
-            return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
-        }
-    }
-    if (args.S <= 32) {
-        args.nqb = 1;
-        const int nblocks = (int)((nbh + 3) / 4);
-        hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 4, 32>), dim3(nblocks), dim3(kThreads), 0, 0, args);
-        return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
-    } else if (args.S <= 64) {
-        args.nqb = 1;
-        const int nblocks = (int)((nbh + 1) / 2);
-        hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 2, 64>), dim3(nblocks), dim3(kThreads), 0, 0, args);
-        return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
+        args.nqb = (args.S + 31) / 32;
+        const int64_t items = (int64_t)args.nqb * nbh;
+        hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
     } else {
-        args.nqb = (args.S + kBr - 1) / kBr;
-        const int nblocks = args.nqb * (int)nbh;
-        hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        args.nqb = 1;
+        if (args.S <= 32)
+            hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 4, 32>), dim3((unsigned)((nbh + 3) / 4)),
+                               dim3(kThreads), 0, 0, args);
+        else
+            hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 2, 64>), dim3((unsigned)((nbh + 1) / 2)),
+                               dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
-    return launch_ok("attn_fwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 }  // namespace

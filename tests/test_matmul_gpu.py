@@ -151,3 +151,18 @@ def test_gemm_256_row_tiles_epilogue():
     y, pre = G.gemm_ex(a, b, bias=bias, act=1)
     assert (np.abs(pre - (exact + bias)) <= bound + 1e-6 * (1 + np.abs(exact))).all()
     np.testing.assert_allclose(y, oracle.gelu_fwd(pre), rtol=1e-5, atol=1e-6)
+
+
+def test_large_row_pitch_takes_the_checked_kernel():
+    """k >= 2^22: the tile-aligned fast path addresses a tile's rows with
+    32-bit byte offsets, so a row pitch this large must go to the generic
+    (64-bit indexed) kernel.  a in {0, 1} and b = 1 make every output an
+    integer below 2^24, exact in any fp32 summation order."""
+    n, m, k = 128, 256, (1 << 22) + 16
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, 2, size=(n, k), dtype=np.uint8).astype(np.float32)
+    b = np.ones((k, m), dtype=np.float32)
+    out = G.gemm_ex(a, b)
+    del b
+    rows = a.sum(axis=1, dtype=np.float64).astype(np.float32)
+    assert np.array_equal(out, np.broadcast_to(rows[:, None], (n, m)))
