@@ -218,6 +218,41 @@ def _timed(ev, fn, reps):
     return sum(ev.elapsed_ms(marks[i], marks[i + 1]) for i in range(reps)) / reps
 
 
+def short_s_study(L, ev, copy_probe_mb, reps=5):
+    """The forward where it is HBM-bound: S = 32, 64, 128 at D = 128, causal,
+    2^20 query rows per tensor (the shapes `secondary` reports); achieved
+    bandwidth counts the algorithmic bytes 16*B*H*S*D + 4*B*H*S.  With
+    copy_probe_mb, one negate_tensor pass over that many MiB follows (known
+    bytes for scaling the traffic counters)."""
+    out = {}
+    rng = np.random.default_rng(7)
+    D = 128
+    for S in (32, 64, 128):
+        B, H = (1 << 20) // S // 64, 64
+        n = B * H * S * D
+        q, k, v = (DeviceArray((n,), rng.standard_normal(n, dtype=np.float32)) for _ in range(3))
+        o, lse = DeviceArray((n,)), DeviceArray((B * H * S,))
+        st = capi.contiguous_strides(B, H, S, D)
+        sc = float(np.float32(1.0 / math.sqrt(D)))
+        ms = _timed(ev, lambda: L.attention_fwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, B, H, S, D, sc, 1,
+                                                *st, *st), reps)
+        capi.check(what=f"short-S forward S={S}")
+        byts = 16 * n + 4 * B * H * S
+        out[f"short_s{S}_fwd"] = {"shape": f"B{B} H{H} S{S} D{D} causal=True", "fwd_ms": round(ms, 4),
+                                  "algorithmic_bytes": byts, "fwd_hbm_gbs": round(byts / ms / 1e6, 1),
+                                  "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
+        del q, k, v, o, lse
+    if copy_probe_mb > 0:
+        n = copy_probe_mb * (1 << 20) // 4
+        src, dst = DeviceArray((n,)), DeviceArray((n,))
+        L.negate_tensor.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        L.negate_tensor(src.ptr, dst.ptr, n)
+        L.sync_device()
+        capi.check(what="copy probe")
+        out["copy_probe_bytes"] = {"read": 4 * n, "write": 4 * n}
+    return out
+
+
 def decoder_step(B, S, d, H, steps):
     """Times config 5's training step; flops: 3 x the forward
     GEMMs (2*B*S*d*d*(3 + 1 + 4 + 4)) plus causal attention fwd+bwd."""
@@ -393,6 +428,10 @@ def main(argv=None):
                     help="after the timed steps, run one plain copy-like kernel "
                          "(negate_tensor: reads and writes N MiB) so rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE can be scaled against known bytes")
+    ap.add_argument("--short-s-study", action="store_true",
+                    help="only run the short-sequence forwards (S = 32, 64, 128; D = 128, causal; "
+                         "the HBM-bound regime) and the copy probe if asked, and print their records "
+                         "(for the rocprofv3 traffic counters)")
     ap.add_argument("--decoder-steps", type=int, default=0,
                     help="only run config 5's decoder-block training step this many "
                          "times and print its record (for profiling)")
@@ -405,6 +444,9 @@ def main(argv=None):
     if args.decoder_steps > 0:
         print(json.dumps({"config5_decoder_step": decoder_step(8, 1024, 1024, 16, args.decoder_steps)}),
               flush=True)
+        return 0
+    if args.short_s_study:
+        print(json.dumps(short_s_study(capi.lib(), HipEvents(), args.copy_probe_mb)), flush=True)
         return 0
 
     B, H, S, D = args.batch, args.heads, args.seq, args.head_dim
