@@ -166,3 +166,25 @@ def test_large_row_pitch_takes_the_checked_kernel():
     del b
     rows = a.sum(axis=1, dtype=np.float64).astype(np.float32)
     assert np.array_equal(out, np.broadcast_to(rows[:, None], (n, m)))
+
+
+@pytest.mark.parametrize("n,m", [(5, 7), (128, 256)])
+def test_empty_inner_dimension_gives_empty_sums(n, m):
+    """k = 0: every output is an empty sum, 0, as in the reference's loop
+    (operators_cpu.c:47-60).  Through the C ABI, and through Tensor @, whose
+    empty operands carry null device pointers; gemm_ex then applies its
+    epilogue to the zeros."""
+    from ember_amd import Tensor
+
+    a = np.zeros((n, 0), np.float32)
+    b = np.zeros((0, m), np.float32)
+    out = G.matmul(a, b)
+    assert out.shape == (n, m) and not out.any()
+    t = Tensor(a) @ Tensor(b)
+    assert t.shape == (n, m) and not t.to_np().any()
+    bias = np.linspace(-2, 2, m).astype(np.float32)
+    res = np.random.default_rng(3).standard_normal((n, m)).astype(np.float32)
+    got, pre = G.gemm_ex(a, b, bias=bias, residual=res, act=1)
+    full = np.ascontiguousarray(np.broadcast_to(bias, (n, m)))
+    assert np.array_equal(pre, full)
+    np.testing.assert_allclose(got, oracle.gelu_fwd(full) + res, rtol=1e-6, atol=1e-6)
