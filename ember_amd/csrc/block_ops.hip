@@ -4,7 +4,9 @@
 //
 //   gelu_bwd: dx = dy * ((1 + tanh(0.8u)) * (0.5 + 0.8(u - y)))
 //             (ember/nn/activations.py:61-66, evaluated in the order of
-//             Ember's element-wise operators; u = GELU input, y = output)
+//             Ember's element-wise operators; u = GELU input, y = output,
+//             recomputed from u with the forward's operations when not
+//             given: 12 instead of 16 bytes per element)
 //   col_sum:  out[c] = sum_r x[r][c], the bias gradient of a Linear layer
 //             (ember/nn/layers.py:54, em.sum(grad_y, axis=0)).  Widths that
 //             are a multiple of 4 (16-byte aligned): a workgroup owns 64
@@ -18,22 +20,50 @@
 #include <math.h>
 
 #include "common.h"
+#include "mfma.h"
 
 namespace ember {
 namespace {
 
+// One element: t = 1 + tanh(0.8u); y = (0.5u) * t when recomputed (the
+// forward's own operations, so the same bits as the stored output);
+// dx = dy * (t * (0.8(u - y) + 0.5)).
+template <bool RECOMPUTE>
+__device__ __forceinline__ float gelu_bwd_one(float dyv, float x, float yv)
+{
+#pragma clang fp contract(off)
+    const float t = tanhf(x * 0.8f) + 1.0f;
+    const float y = RECOMPUTE ? (x * 0.5f) * t : yv;
+    const float r = (x - y) * 0.8f + 0.5f;
+    return dyv * (t * r);
+}
+
+// n % 4 == 0 and 16-byte aligned operands: float4 per thread and pass.
+template <bool RECOMPUTE>
+__global__ __launch_bounds__(256) void gelu_bwd_vec4(const float *__restrict__ dy, const float *__restrict__ u,
+                                                     const float *__restrict__ y, float *__restrict__ dx,
+                                                     int64_t n4)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        const f32x4 g = ((const f32x4 *)dy)[i];
+        const f32x4 x = ((const f32x4 *)u)[i];
+        f32x4 yv = {0.f, 0.f, 0.f, 0.f};
+        if (!RECOMPUTE) yv = ((const f32x4 *)y)[i];
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = gelu_bwd_one<RECOMPUTE>(g[j], x[j], yv[j]);
+        ((f32x4 *)dx)[i] = o;
+    }
+}
+
+template <bool RECOMPUTE>
 __global__ __launch_bounds__(256) void gelu_bwd_kernel(const float *__restrict__ dy,
                                                        const float *__restrict__ u,
                                                        const float *__restrict__ y,
                                                        float *__restrict__ dx, int64_t n)
 {
-#pragma clang fp contract(off)
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-        const float x = u[i];
-        const float t = tanhf(x * 0.8f) + 1.0f;
-        const float r = (x - y[i]) * 0.8f + 0.5f;
-        dx[i] = dy[i] * (t * r);
-    }
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        dx[i] = gelu_bwd_one<RECOMPUTE>(dy[i], u[i], RECOMPUTE ? 0.0f : y[i]);
 }
 
 constexpr int kRowsPerSlice = 128;
@@ -105,11 +135,21 @@ extern "C" int gelu_bwd(const float *dy, const float *u, const float *y, float *
     using namespace ember;
     if (n < 0) return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd");
     if (n == 0) return EMBER_OK;
-    if (!dy || !u || !y || !dx) return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd");
-    int64_t blocks = (n + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(gelu_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, 0, dy, u, y, dx, n);
-    return launch_ok("gelu_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+    if (!dy || !u || !dx) return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd");
+    const bool vec = n % 4 == 0 && (((uintptr_t)dy | (uintptr_t)u | (uintptr_t)y | (uintptr_t)dx) % 16) == 0;
+    const int64_t work = vec ? n / 4 : n;
+    // About 8 workgroups per CU, each thread a few elements (grid-stride).
+    int64_t blocks = (work + 255) / 256;
+    const int64_t cap = 8 * 256;
+    if (blocks > cap) blocks = cap;
+    if (vec) {
+        if (y) hipLaunchKernelGGL(gelu_bwd_vec4<false>, dim3((unsigned)blocks), dim3(256), 0, 0, dy, u, y, dx, work);
+        else hipLaunchKernelGGL(gelu_bwd_vec4<true>, dim3((unsigned)blocks), dim3(256), 0, 0, dy, u, y, dx, work);
+    } else {
+        if (y) hipLaunchKernelGGL(gelu_bwd_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, 0, dy, u, y, dx, work);
+        else hipLaunchKernelGGL(gelu_bwd_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, 0, dy, u, y, dx, work);
+    }
+    return launch_ok("gelu_bwd") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 extern "C" int col_sum(const float *x, float *out, int64_t rows, int64_t cols)

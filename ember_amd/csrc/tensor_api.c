@@ -738,18 +738,28 @@ static PyObject *py_gemm(PyObject *module, PyObject *args)
     return (PyObject *)out;
 }
 
+/* _gelu_bwd(dy, u, y=None): y None recomputes the GELU output from u. */
 static PyObject *py_gelu_bwd(PyObject *module, PyObject *args)
 {
-    TensorObject *dy, *u, *y;
+    TensorObject *dy, *u;
+    PyObject *yo = Py_None;
     (void)module;
-    if (!PyArg_ParseTuple(args, "O!O!O!", &TensorType, &dy, &TensorType, &u, &TensorType, &y)) return NULL;
-    if (dy->size != u->size || y->size != u->size) {
+    if (!PyArg_ParseTuple(args, "O!O!|O", &TensorType, &dy, &TensorType, &u, &yo)) return NULL;
+    TensorObject *y = NULL;
+    if (yo != Py_None) {
+        if (!PyObject_TypeCheck(yo, &TensorType)) {
+            PyErr_SetString(PyExc_TypeError, "_gelu_bwd: y must be a _Tensor or None");
+            return NULL;
+        }
+        y = (TensorObject *)yo;
+    }
+    if (dy->size != u->size || (y && y->size != u->size)) {
         PyErr_SetString(PyExc_ValueError, "_gelu_bwd: size mismatch");
         return NULL;
     }
     TensorObject *dx = alloc_tensor(u->size);
     if (!dx) return NULL;
-    int st = gelu_bwd(dy->d_ptr, u->d_ptr, y->d_ptr, dx->d_ptr, u->size);
+    int st = gelu_bwd(dy->d_ptr, u->d_ptr, y ? y->d_ptr : NULL, dx->d_ptr, u->size);
     if (raise_status(st, "_gelu_bwd")) {
         Py_DECREF(dx);
         return NULL;

@@ -194,8 +194,9 @@ class Linear(Layer):
         if self.x is None:
             raise RuntimeError("forward() must run before backward()")
         if self.activation == "gelu":
-            grad_y = Tensor._from_core(C._gelu_bwd(grad_y._core, self.pre._core, self.y._core),
-                                       grad_y.shape)
+            # The GELU output is recomputed from the pre-activation in the
+            # kernel (bit-identical to the forward's).
+            grad_y = Tensor._from_core(C._gelu_bwd(grad_y._core, self.pre._core), grad_y.shape)
         self.grad_w = weight_grad(self.x, grad_y)
         self.grad_b = col_sum(grad_y)
         return input_grad(grad_y, self.w)
@@ -336,7 +337,7 @@ class DecoderBlock(Layer):
         # MLP: y = x2 + GELU(h2 W1 + b1) W2 + b2
         g_w2, g_b2 = weight_grad(a, grad_y), col_sum(grad_y)
         da = input_grad(grad_y, self.w_2)
-        du = Tensor._from_core(C._gelu_bwd(da._core, u._core, a._core), da.shape)
+        du = Tensor._from_core(C._gelu_bwd(da._core, u._core), da.shape)  # a recomputed from u
         g_w1, g_b1 = weight_grad(h2, du), col_sum(du)
         dx2 = self.ln2.backward(input_grad(du, self.w_1), residual=grad_y)
         # attention: x2 = x + O Wo + bo

@@ -178,7 +178,10 @@ int gemm_ex(const float *a, const float *b, float *out, int batch, int n, int m,
             int trans_a, int trans_b, const float *bias, const float *residual, float *pre, int act);
 
 /* dx = dy * ((1 + tanh(0.8u)) * (0.5 + 0.8(u - y))): the backward of Ember's
- * GELU (ember/nn/activations.py:61-66) with u its input and y its output. */
+ * GELU (ember/nn/activations.py:61-66) with u its input and y its output.
+ * y may be NULL: it is then recomputed from u as (0.5u)(1 + tanh(0.8u)),
+ * the forward's own fp32 operations, so dx is bit-identical to passing the
+ * stored output (and one array less is read). */
 int gelu_bwd(const float *dy, const float *u, const float *y, float *dx, int64_t n);
 
 /* out[c] = sum over rows of x[r][c] (x is rows x cols): a Linear layer's bias

@@ -81,6 +81,29 @@ def test_gelu_bwd_and_col_sum():
         np.testing.assert_allclose(got.to_np(), x.astype(np.float64).sum(0), rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("n", [4096 * 33, 5001])
+def test_gelu_bwd_recomputed_output_is_bitwise_the_stored_one(n):
+    """_gelu_bwd(dy, u) recomputes the GELU output from u: bit-identical to
+    passing the output that the GEMM epilogue or the composed GELU layer
+    stored (float4 path for n % 4 == 0, scalar path otherwise)."""
+    u = rnd((n,), 15, 3.0)
+    dy = rnd((n,), 16)
+    tu, tdy = Tensor(u), Tensor(dy)
+    y_layer = nn.GELU()(tu)                                   # composed element-wise operators
+    got = _core._gelu_bwd(tdy._core, tu._core)._to_np()
+    stored = _core._gelu_bwd(tdy._core, tu._core, y_layer._core)._to_np()
+    assert np.array_equal(got, stored)
+    np.testing.assert_allclose(got, oracle.gelu_bwd(dy, u, oracle.gelu_fwd(u)), rtol=1e-5, atol=1e-6)
+    if n % 1024 == 0:   # through the GEMM epilogue: out = GELU(pre), pre = x @ I
+        rows = n // 1024
+        xm = u.reshape(rows, 1024)
+        y_epi, pre = nn.linear(Tensor(xm), Tensor(np.eye(1024, dtype=np.float32)), None, None, True)
+        assert np.array_equal(pre.to_np(), xm)
+        got2 = _core._gelu_bwd(tdy._core, pre._core)._to_np()
+        stored2 = _core._gelu_bwd(tdy._core, pre._core, y_epi._core)._to_np()
+        assert np.array_equal(got2, stored2) and np.array_equal(got2, got)
+
+
 def _gpu_block_params(block):
     return [p.to_np().astype(np.float64) for p in block.parameters()]
 
