@@ -372,19 +372,27 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb) bt[cb] = *(const f32x4 *)&bs[bbase + cb * 32 * FASTR + kk];
             }
+            if (TB) {
+                // Column block outermost: the MFMAs of block cb need only its
+                // own B read, so the later reads overlap earlier products
+                // (k-step innermost would need all four reads before the
+                // first MFMA: 12 % slower with one workgroup per CU).  Each
+                // accumulator still adds its k-steps in the same order.
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                f32x4 bf;
-                if (TB) {
+                for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-                    for (int cb = 0; cb < 4; ++cb) bf[cb] = bt[cb][j];
-                } else {
-                    bf = *(const f32x4 *)&bs[bbase + (kk + j) * FN];
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[rb][cb] = mfma_32x32x2(af[rb][j], bt[cb][j], acc[rb][cb]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 bf = *(const f32x4 *)&bs[bbase + (kk + j) * FN];
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_32x32x2(af[rb][j], bf[cb], acc[rb][cb]);
                 }
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                    for (int cb = 0; cb < 4; ++cb) acc[rb][cb] = mfma_32x32x2(af[rb][j], bf[cb], acc[rb][cb]);
             }
         }
     };
