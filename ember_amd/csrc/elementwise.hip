@@ -174,6 +174,31 @@ __global__ void k_sum_partial(const float *a, int size, double *partial)
     if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
 }
 
+// The MSE loss in one pass: d = p - t; grad = d * scale; partial sums of
+// d*d exactly as k_sum_partial forms them over the product tensor (same
+// grid, same strided walk, same tree), so the loss equals
+// sum(diff * diff) and grad equals scale * diff bit for bit.
+__global__ void k_mse_partial(const float *p, const float *t, float *grad, float scale, int size,
+                              double *partial)
+{
+#pragma clang fp contract(off)
+    __shared__ double red[kBlock];
+    double s = 0.0;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < size; i += gridDim.x * blockDim.x) {
+        const float d = p[i] - t[i];
+        grad[i] = d * scale;
+        const float sq = d * d;
+        s += (double)sq;
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = kBlock / 2; off > 0; off >>= 1) {
+        if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
 __global__ void k_sum_final(const double *partial, int n, float *out)
 {
     __shared__ double red[kBlock];
@@ -268,6 +293,25 @@ float sum(const float *a, int size)
     float host = 0.0f;
     ember::hip_ok(hipMemcpy(&host, res, sizeof(float), hipMemcpyDeviceToHost), "sum");
     return host;
+}
+
+int mse_loss(const float *pred, const float *target, float *grad, int size, float scale, float *loss)
+{
+    if (size < 0 || !loss) return ember::record_error(EMBER_ERR_INVALID_ARGUMENT, "mse_loss");
+    *loss = 0.0f;
+    if (size == 0) return EMBER_OK;
+    if (!pred || !target || !grad) return ember::record_error(EMBER_ERR_INVALID_ARGUMENT, "mse_loss");
+    const int nblk = grid_for(size) > 1024 ? 1024 : grid_for(size);  // as in sum()
+    char *ws = (char *)ember::scratch(ember::kScratchSum, (size_t)nblk * sizeof(double) + 16);
+    if (!ws) return EMBER_ERR_OUT_OF_MEMORY;
+    double *partial = (double *)ws;
+    float *res = (float *)(ws + (size_t)nblk * sizeof(double));
+    hipLaunchKernelGGL(k_mse_partial, dim3(nblk), dim3(kBlock), 0, 0, pred, target, grad, scale, size, partial);
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(kBlock), 0, 0, partial, nblk, res);
+    if (!ember::launch_ok("mse_loss")) return EMBER_ERR_DEVICE;
+    if (!ember::hip_ok(hipMemcpy(loss, res, sizeof(float), hipMemcpyDeviceToHost), "mse_loss"))
+        return EMBER_ERR_DEVICE;
+    return EMBER_OK;
 }
 
 int sum_axis_product(const int *shape, int start, int end)

@@ -497,6 +497,30 @@ static PyObject *py_sum(PyObject *module, PyObject *args)
     return PyFloat_FromDouble((double)s);
 }
 
+/* _mse_loss(pred, target, scale) -> (sum of squared differences, grad):
+ * one pass for MSELoss (see mse_loss). */
+static PyObject *py_mse_loss(PyObject *module, PyObject *args)
+{
+    TensorObject *p, *t;
+    float scale;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!f", &TensorType, &p, &TensorType, &t, &scale)) return NULL;
+    if (p->size != t->size) {
+        PyErr_SetString(PyExc_ValueError, "_mse_loss: size mismatch");
+        return NULL;
+    }
+    if (!fits_int(p->size, "_mse_loss")) return NULL;
+    TensorObject *g = alloc_tensor(p->size);
+    if (!g) return NULL;
+    float loss = 0.0f;
+    int st = mse_loss(p->d_ptr, t->d_ptr, g->d_ptr, (int)p->size, scale, &loss);
+    if (raise_status(st, "_mse_loss")) {
+        Py_DECREF(g);
+        return NULL;
+    }
+    return Py_BuildValue("(dN)", (double)loss, (PyObject *)g);
+}
+
 typedef void (*axis_fn)(const float *, float *, int, int, int);
 
 static PyObject *do_axis(PyObject *args, axis_fn fn, const char *what)
@@ -1012,6 +1036,7 @@ static PyMethodDef module_methods[] = {
     METHOD("_transpose", py_transpose, "2-D transpose"),
     METHOD("_from_numpy", py_from_numpy, "float32 C-contiguous buffer -> _Tensor"),
     METHOD("_sum", py_sum, "sum of all elements"),
+    METHOD("_mse_loss", py_mse_loss, "MSE loss sum and gradient in one pass"),
     METHOD("_sum_axis", py_sum_axis, "sum over one axis"),
     METHOD("_max_axis", py_max_axis, "max over one axis"),
     METHOD("_softmax", py_softmax, "softmax along one axis, one launch"),

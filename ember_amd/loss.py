@@ -4,26 +4,39 @@ from __future__ import annotations
 
 import math
 
+from ember_amd import _core as C
 from ember_amd.tensor import Tensor, amax, exp, log, sum as _sum
 
 
 class MSELoss:
     """Mean squared error over all elements (``losses.py:9-26``):
-    forward returns mean((pred - target)^2), backward (2/n)*(pred - target)."""
+    forward returns mean((pred - target)^2), backward (2/n)*(pred - target).
+
+    Equal shapes take one fused pass (``_mse_loss``) that returns the same
+    float sum as ``sum(diff * diff)`` and the gradient ``(2/n) * diff`` bit
+    for bit; broadcasting shapes compose the operators as the reference."""
 
     def __init__(self) -> None:
         self.diff: Tensor | None = None
+        self.grad: Tensor | None = None
         self.n = 0
 
     def forward(self, pred: Tensor, target: Tensor) -> float:
-        self.diff = pred - target
         self.n = math.prod(pred.shape)
+        if isinstance(pred, Tensor) and isinstance(target, Tensor) and pred.shape == target.shape:
+            total, g = C._mse_loss(pred._core, target._core, 2.0 / self.n if self.n else 0.0)
+            self.diff, self.grad = None, Tensor._from_core(g, pred.shape)
+            return total / self.n
+        self.grad = None
+        self.diff = pred - target
         return _sum(self.diff * self.diff) / self.n
 
     def __call__(self, pred: Tensor, target: Tensor) -> float:
         return self.forward(pred, target)
 
     def backward(self) -> Tensor:
+        if self.grad is not None:
+            return self.grad
         if self.diff is None:
             raise RuntimeError("forward() must run before backward()")
         return (2.0 / self.n) * self.diff

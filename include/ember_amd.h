@@ -87,6 +87,14 @@ void transpose(const float *a, float *out, int n, int m);
 /* Sum of all elements; replaces operators_gpu.cu:153-166 (the device
  * reduction is summed in a fixed tree order, not sequentially). */
 float sum(const float *a, int size);
+
+/* Ember's MSELoss in one pass (ember/loss/losses.py:19-26): grad[i] =
+ * (pred[i] - target[i]) * scale and *loss = sum over i of (pred - target)^2,
+ * computed exactly as sum(diff * diff) above (same partition and order), so
+ * with scale = fp32(2/n) both are bit-identical to the composed operators.
+ * No reference counterpart as one symbol: it fuses sub_tensor, mul_tensor,
+ * sum and mul_scalar.  Synchronises (the loss is read back). */
+int mse_loss(const float *pred, const float *target, float *grad, int size, float scale, float *loss);
 /* Product of shape[start:end]; replaces operators_gpu.cu:168-173. */
 int sum_axis_product(const int *shape, int start, int end);
 /* Reduce the middle axis of (outer, axis_dim, inner); sequential fp32 sum /

@@ -91,3 +91,26 @@ def test_cross_entropy_forward_backward():
     lp -= np.log(np.exp(lp).sum(-1, keepdims=True))
     assert value == pytest.approx(-(target * lp).sum() / B, rel=1e-5)
     np.testing.assert_allclose(grad, (np.exp(lp) - target) / B, rtol=1e-5, atol=1e-8)
+
+
+@pytest.mark.parametrize("shape", [(8192, 1024), (3, 7), (1000003,)])
+def test_mse_fused_pass_is_bitwise_the_composed_operators(shape):
+    """MSELoss with equal shapes runs one fused pass; its loss equals
+    sum(diff * diff) / n and its gradient (2 / n) * diff of the composed
+    operators (losses.py:19-26) bit for bit, and both match float64."""
+    pred, target = rnd(shape, 21), rnd(shape, 22)
+    mse = loss.MSELoss()
+    value = mse(Tensor(pred), Tensor(target))
+    grad = mse.backward().to_np()
+    diff = Tensor(pred) - Tensor(target)
+    n = int(np.prod(shape))
+    assert value == em.sum(diff * diff) / n
+    assert np.array_equal(grad, ((2.0 / n) * diff).to_np())
+    d64 = pred.astype(np.float64) - target.astype(np.float64)
+    assert value == pytest.approx((d64 * d64).sum() / n, rel=1e-6)
+    # Broadcasting targets still compose the reference's operators.
+    if len(shape) == 2:
+        row = rnd((1, shape[1]), 23)
+        value_b = loss.MSELoss()(Tensor(pred), Tensor(row))
+        d = pred.astype(np.float64) - row
+        assert value_b == pytest.approx((d * d).sum() / n, rel=1e-6)
