@@ -202,8 +202,25 @@ __global__ __launch_bounds__(256) void ln_param_grad_kernel(const float *__restr
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (quad < nq) {
         const int which = (4 * quad) / d, col = 4 * quad - which * d;
-        for (int b = g; b < nblk; b += kPgGroups) {
-            const float4 v = *(const float4 *)(part + ((int64_t)b * 2 + which) * d + col);
+        const float *src = part + (int64_t)which * d + col;
+        const int64_t step = (int64_t)kPgGroups * 2 * d;  // floats between a thread's rows
+        int b = g;
+        // Eight loads in flight, then the adds in row order (the same sums
+        // as one row at a time).
+        for (; b + 7 * kPgGroups < nblk; b += 8 * kPgGroups) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *(const float4 *)(src + (int64_t)b * 2 * d + u * step);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                s.x += v[u].x;
+                s.y += v[u].y;
+                s.z += v[u].z;
+                s.w += v[u].w;
+            }
+        }
+        for (; b < nblk; b += kPgGroups) {
+            const float4 v = *(const float4 *)(src + (int64_t)b * 2 * d);
             s.x += v.x;
             s.y += v.y;
             s.z += v.z;
