@@ -93,7 +93,22 @@ __global__ __launch_bounds__(256) void col_reduce4(const float *__restrict__ x, 
     const int64_t r1 = r0 + rpw < rows ? r0 + rpw : rows;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (4 * quad < cols) {
-        for (int64_t r = r0 + g; r < r1; r += kGroups) {
+        int64_t r = r0 + g;
+        // Eight rows in flight, then the adds in row order (the same sums as
+        // one row at a time).
+        for (; r + 7 * kGroups < r1; r += 8 * kGroups) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *(const float4 *)(x + (r + u * kGroups) * cols + 4 * quad);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                s.x += v[u].x;
+                s.y += v[u].y;
+                s.z += v[u].z;
+                s.w += v[u].w;
+            }
+        }
+        for (; r < r1; r += kGroups) {
             const float4 v = *(const float4 *)(x + r * cols + 4 * quad);
             s.x += v.x;
             s.y += v.y;
