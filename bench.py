@@ -339,11 +339,16 @@ def secondary(L, ev):
             for n in shapes]
     nparam = sum(shapes)
     t_box = [0]
+    # Pointer tables built once, so that the host keeps ahead of the GPU and
+    # the events time the kernel, not Python (building them per call takes
+    # about as long as the ~60 us launch).
+    nt = len(shapes)
+    tables = [(C.c_void_p * nt)(*(x[j].ptr for x in tens)) for j in range(4)]
+    sizes = (C.c_int64 * nt)(*shapes)
 
     def adam():
         t_box[0] += 1
-        return capi.adam_step([x[0] for x in tens], [x[1] for x in tens], [x[2] for x in tens],
-                              [x[3] for x in tens], 1e-3, 0.9, 0.999, 1e-8, t_box[0])
+        return L.adam_step(*tables, sizes, nt, 1e-3, 0.9, 0.999, 1e-8, t_box[0])
 
     ms = _timed(ev, adam, 20)
     capi.check(what="adam_step")
