@@ -238,3 +238,57 @@ def test_packed_qkv_layout(S, D):
     assert np.array_equal(g[:, :, 1].transpose(0, 2, 1, 3), dk_ref)
     assert np.array_equal(g[:, :, 2].transpose(0, 2, 1, 3), dv_ref)
     np.testing.assert_allclose(g[:, :, 0].transpose(0, 2, 1, 3), dq_ref, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------ long sequences
+
+
+def _f64_reference(q, k, v, d_o, causal, scale, chunk=1024):
+    """float64 O and LSE of every row of one head, streamed over row chunks
+    (the S x S scores of a chunk at a time), and Delta = rowsum(dO * O)."""
+    S, D = q.shape
+    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    o = np.empty((S, D))
+    lse = np.empty(S)
+    for r0 in range(0, S, chunk):
+        r1 = min(S, r0 + chunk)
+        nk = r1 if causal else S
+        s = (q64[r0:r1] @ k64[:nk].T) * scale
+        if causal:
+            s[np.arange(r1 - r0)[:, None] + r0 < np.arange(nk)[None, :]] = -np.inf
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        l = p.sum(axis=1, keepdims=True)
+        o[r0:r1] = (p @ v64[:nk]) / l
+        lse[r0:r1] = (m + np.log(l))[:, 0]
+    delta = (d_o.astype(np.float64) * o).sum(axis=1)
+    return o, lse, delta
+
+
+@pytest.mark.parametrize("S,D,causal", [(16384, 128, True), (8192, 64, False)])
+def test_long_sequence_against_float64(S, D, causal):
+    """The longest loops (S/32 query blocks per key block): O and LSE of every
+    row, dQ of sampled rows and dK, dV of sampled keys against a float64
+    NumPy evaluation of the same formulas (closed-form gradients)."""
+    q, k, v, d_o = _inputs(1, 1, S, D, seed=1100 + D)
+    scale = G.scale_for(D)
+    o, lse = G.attention_fwd(q, k, v, causal)
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    q0, k0, v0, g0 = q[0, 0], k[0, 0], v[0, 0], d_o[0, 0]
+    o_r, lse_r, delta = _f64_reference(q0, k0, v0, g0, causal, scale)
+    np.testing.assert_allclose(o[0, 0], o_r, **TOL)
+    np.testing.assert_allclose(lse[0, 0], lse_r, **TOL)
+    q64, k64, v64, g64 = (x.astype(np.float64) for x in (q0, k0, v0, g0))
+    picks = sorted({0, 1, 31, 32, 127, 128, S // 2, S - 129, S - 33, S - 1}
+                   | set(np.random.default_rng(S).choice(S, 16, replace=False).tolist()))
+    for i in picks:  # dQ_i = scale sum_j P_ij (dO_i . V_j - Delta_i) K_j
+        nk = i + 1 if causal else S
+        p = np.exp(scale * (k64[:nk] @ q64[i]) - lse_r[i])
+        ds = p * (v64[:nk] @ g64[i] - delta[i])
+        np.testing.assert_allclose(dq[0, 0, i], scale * (ds @ k64[:nk]), err_msg=f"dQ row {i}", **TOL)
+    for j in picks:  # dV_j = sum_i P_ij dO_i, dK_j = scale sum_i dS_ij Q_i
+        i0 = j if causal else 0
+        p = np.exp(scale * (q64[i0:] @ k64[j]) - lse_r[i0:])
+        ds = p * (g64[i0:] @ v64[j] - delta[i0:])
+        np.testing.assert_allclose(dv[0, 0, j], p @ g64[i0:], err_msg=f"dV row {j}", **TOL)
+        np.testing.assert_allclose(dk[0, 0, j], scale * (ds @ q64[i0:]), err_msg=f"dK row {j}", **TOL)
