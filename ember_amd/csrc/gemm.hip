@@ -13,7 +13,10 @@
 // double (src/tensor/operators_cpu.c:47-60); agreement is to fp32 rounding
 // of a length-k sum, see the parity tests.
 //
-// Tiling: a workgroup of 4 waves computes a 128 x 128 block of out, each
+// Tile-aligned shapes (n % 128, m % 256, k % 16 == 0) take the fast path
+// further down (gemm_f32_dma_kernel: 128 x 256 or 256 x 256 tiles, slabs
+// copied HBM -> LDS without registers).  The general path, for any other
+// shape: a workgroup of 4 waves computes a 128 x 128 block of out, each
 // wave a 64 x 64 quadrant as 2 x 2 MFMA accumulators.  The k dimension is
 // walked in 32-wide slabs: the next slab's A (128 x 32) and B (32 x 128)
 // are loaded from HBM/L2 into registers while the current one is multiplied
