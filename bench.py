@@ -1,6 +1,6 @@
 """Benchmark: fused causal attention forward+backward, fp32, on one MI355X.
 
-Workload (the config the metric is quoted on):
+Workload (the configuration the headline metric is quoted on):
 B=4, H=32, S=4096, D=128, causal, Q/K/V/dO ~ N(0,1) seeded, scale 1/sqrt(D).
 One step = attention_fwd + attention_bwd through the C ABI of
 libember_amd.so on inputs already resident in HBM.
