@@ -292,3 +292,31 @@ def test_long_sequence_against_float64(S, D, causal):
         ds = p * (g64[i0:] @ v64[j] - delta[i0:])
         np.testing.assert_allclose(dv[0, 0, j], p @ g64[i0:], err_msg=f"dV row {j}", **TOL)
         np.testing.assert_allclose(dk[0, 0, j], scale * (ds @ q64[i0:]), err_msg=f"dK row {j}", **TOL)
+
+
+@pytest.mark.parametrize("D,causal", [(128, True), (64, False)])
+def test_known_answers_at_full_length(D, causal):
+    """Closed forms at S = 4096 on the HIP kernels themselves: K = 0 makes
+    every score equal, so row i averages V[0..i] (causal) or all of V, with
+    LSE = ln(i+1) or ln(S); V = 1 gives O = 1; and (non-causal) permuting
+    keys together with values leaves O and LSE unchanged."""
+    S = 4096
+    q, k, v, _ = _inputs(1, 2, S, D, seed=1200 + D)
+    o, lse = G.attention_fwd(q, np.zeros_like(k), v, causal)
+    v64 = v.astype(np.float64)
+    if causal:
+        mean = np.cumsum(v64, axis=2) / np.arange(1, S + 1)[None, None, :, None]
+        ln_n = np.log(np.arange(1, S + 1, dtype=np.float64))
+    else:
+        mean = np.broadcast_to(v64.mean(axis=2, keepdims=True), v64.shape)
+        ln_n = np.full(S, np.log(S))
+    np.testing.assert_allclose(o, mean, **TOL)
+    np.testing.assert_allclose(lse, np.broadcast_to(ln_n, lse.shape), rtol=1e-6, atol=1e-6)
+    o1, _ = G.attention_fwd(q, k, np.ones_like(v), causal)
+    np.testing.assert_allclose(o1, 1.0, rtol=0, atol=1e-5)
+    if not causal:
+        perm = np.random.default_rng(D).permutation(S)
+        o2, lse2 = G.attention_fwd(q, k[:, :, perm], v[:, :, perm], causal)
+        o3, lse3 = G.attention_fwd(q, k, v, causal)
+        np.testing.assert_allclose(o2, o3, **TOL)
+        np.testing.assert_allclose(lse2, lse3, **TOL)
