@@ -267,20 +267,28 @@ template <bool TB> struct BSlab {
 
 // TM = 128 (4 waves, 2 workgroups per CU) or 256 (8 waves, 1 per CU: the
 // same 64 x 128 per wave, a third less L2 -> LDS traffic per flop).
-template <bool TA, bool TB, bool SPLIT, int TM = FM>
-__global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel(GemmArgs g)
+// KG = 2 (TM = 128 only): two groups of 4 waves per workgroup, one per CU,
+// each group with its own LDS buffers and the whole 128 x 256 tile; group 0
+// multiplies the even k-slabs, group 1 the odd ones, and group 1's sums are
+// added to group 0's through LDS before the store.  For outputs with no more
+// tiles than CUs: two waves per SIMD instead of one, no extra HBM traffic.
+template <bool TA, bool TB, bool SPLIT, int TM = FM, int KG = 1>
+__global__ __launch_bounds__(TM * 2 * KG, TM == 128 && KG == 1 ? 2 : 1) void gemm_f32_dma_kernel(GemmArgs g)
 {
-    constexpr int NW = TM / 32;  // waves: TM/64 rows x 2 columns of 64 x 128
+    static_assert(KG == 1 || (KG == 2 && TM == 128 && !SPLIT), "k groups: 128-row tiles, no split-K");
+    constexpr int NW = TM / 32;  // waves per group: TM/64 rows x 2 columns of 64 x 128
     constexpr int ABUF = ASlab<TA, TM>::kBuf, BBUF_ = BSlab<TB>::kBuf;
     constexpr int ACOP = ASlab<TA, TM>::kCopies, BCOP = BSlab<TB>::kCopies;
-    __shared__ float As0[ABUF], As1[ABUF];
-    __shared__ float Bs0[BBUF_], Bs1[BBUF_];
+    __shared__ float As0[KG * ABUF], As1[KG * ABUF];
+    __shared__ float Bs0[KG * BBUF_], Bs1[KG * BBUF_];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     // Wave index made provably uniform: the per-wave copy counts and LDS
     // destinations below then use scalar branches and registers.
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grpk = KG == 1 ? 0 : wg / NW;  // k group
+    const int w = KG == 1 ? wg : wg - grpk * NW;  // wave within the group
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
     const int wr = w >> 1, wc = w & 1;
@@ -400,25 +408,64 @@ __global__ __launch_bounds__(TM * 2, TM == 128 ? 2 : 1) void gemm_f32_dma_kernel
         }
     };
 
-    const int nslab = (kend - kbeg) / FK;
+    // This group's buffers and slabs: slab j of the group is slab
+    // KG*j + grpk of the tile (the host launches KG = 2 only when the slab
+    // count is even, so both groups meet the same barriers).
+    float *const as0 = As0 + grpk * ABUF, *const as1 = As1 + grpk * ABUF;
+    float *const bs0 = Bs0 + grpk * BBUF_, *const bs1 = Bs1 + grpk * BBUF_;
+    const int nslab = (kend - kbeg) / FK / KG;
+    auto kslab = [&](int j) { return kbeg + (KG * j + grpk) * FK; };
     if (nslab > 0) {
-        fetch(kbeg, As0, Bs0);
+        fetch(kslab(0), as0, bs0);
         wait_vmem();
         __syncthreads();
     }
     // Two slabs per trip so that each buffer is a distinct LDS object: the
     // compiler then knows the copy into one does not feed reads of the other.
     for (int s = 0; s < nslab; s += 2) {
-        if (s + 1 < nslab) fetch(kbeg + (s + 1) * FK, As1, Bs1);
-        slab(As0, Bs0);
+        if (s + 1 < nslab) fetch(kslab(s + 1), as1, bs1);
+        slab(as0, bs0);
         wait_vmem();
         __syncthreads();
         if (s + 1 < nslab) {
-            if (s + 2 < nslab) fetch(kbeg + (s + 2) * FK, As0, Bs0);
-            slab(As1, Bs1);
+            if (s + 2 < nslab) fetch(kslab(s + 2), as0, bs0);
+            slab(as1, bs1);
             wait_vmem();
             __syncthreads();
         }
+    }
+    if constexpr (KG == 2) {
+        // Group 1's sums to group 0, one row block at a time through the B
+        // buffers (free after the loop's last barrier): wave w of group 1
+        // writes acc[rb][0..3] lane-linearly (4096 floats) at xb, the wave
+        // of group 0 with the same w reads them back.  Sums in a fixed order
+        // (even slabs + odd slabs).
+        static_assert(2 * BBUF_ >= 2 * 4096, "exchange area: two waves per B buffer");
+        float *const xb = (w < 2 ? Bs0 : Bs1) + (w & 1) * 4096 + 4 * lane;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            if (grpk == 1) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *(f32x4 *)&xb[(cb * 4 + q) * 256] =
+                            f32x4{acc[rb][cb][4 * q], acc[rb][cb][4 * q + 1], acc[rb][cb][4 * q + 2], acc[rb][cb][4 * q + 3]};
+            }
+            __syncthreads();
+            if (grpk == 0) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x4 o = *(const f32x4 *)&xb[(cb * 4 + q) * 256];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[rb][cb][4 * q + e] += o[e];
+                    }
+            }
+            __syncthreads();
+        }
+        if (grpk == 1) return;
     }
 
     // Output: row(rb, i) and col(cb) as the operand layouts above define them.
@@ -530,10 +577,17 @@ void launch_fast(const GemmArgs &g, dim3 grid, bool split)
             }
         }
     }
-    if (split)
+    if (split) {
         hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, true>), grid, dim3(kThreads), 0, 0, g);
-    else
-        hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, false>), grid, dim3(kThreads), 0, 0, g);
+        return;
+    }
+    // No more tiles than CUs: one workgroup per CU either way, so give it two
+    // k groups (two waves per SIMD); needs an even slab count.
+    if ((int)(grid.x * grid.y) <= num_cus() && (g.k / FK) % 2 == 0 && g.k >= 4 * FK) {
+        hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, false, FM, 2>), grid, dim3(2 * kThreads), 0, 0, g);
+        return;
+    }
+    hipLaunchKernelGGL((gemm_f32_dma_kernel<TA, TB, false>), grid, dim3(kThreads), 0, 0, g);
 }
 
 int gemm_launch(const float *a, const float *b, float *out, int batch, int n, int m, int k,
