@@ -1,0 +1,89 @@
+"""A fixed-seed sweep of attention shapes and layouts against the CPU oracle.
+
+Each case draws B, H, S, D, the mask and a layout: rows padded past D and
+heads padded past S (strides that are not those of a contiguous tensor),
+separately for the q/k/v/dq/dk/dv and the o/dO triples, so the kernels'
+stride arithmetic, tile tails and launch choices (split-key, packed, wave
+and workgroup forwards) meet shapes no hand-written case lists.  Tolerance
+as everywhere: max-abs 2e-4 / rel 1e-3; padding must stay untouched.
+"""
+
+import numpy as np
+import pytest
+
+import gpu_helpers as G
+import oracle
+from ember_amd import capi
+from ember_amd.capi import DeviceArray
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(rtol=1e-3, atol=2e-4)
+SENTINEL = np.float32(12345.0)
+
+
+def _case(seed):
+    rng = np.random.default_rng(10_000 + seed)
+    B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+    S = int(rng.choice([1, 2, 5, 31, 32, 33, 64, 65, 100, 127, 128, 129, 200, 256, 300, 513, 700]))
+    D = int(rng.choice([32, 64, 128]))
+    causal = bool(rng.integers(0, 2))
+    pads = [int(rng.choice([0, 4, 12, 32])) for _ in range(2)]  # row padding (floats) per triple
+    hpads = [int(rng.choice([0, 1, 3])) for _ in range(2)]       # extra rows per head per triple
+    return B, H, S, D, causal, pads, hpads
+
+
+def _strided(B, H, S, D, pad, hpad):
+    """Strides (sb, sh, ss) of a (B, H, S + hpad, D + pad) buffer."""
+    ss = D + pad
+    sh = (S + hpad) * ss
+    return (H * sh, sh, ss), B * H * sh
+
+
+def _upload(x, strides, total):
+    """x (B, H, S, D) into a padded device buffer; padding = SENTINEL."""
+    B, H, S, D = x.shape
+    buf = np.full(total, SENTINEL, np.float32)
+    view = np.lib.stride_tricks.as_strided(buf, shape=x.shape, strides=tuple(4 * s for s in strides) + (4,))
+    view[...] = x
+    return DeviceArray.from_numpy(buf), buf
+
+
+def _download(dev, strides, shape):
+    buf = dev.numpy()
+    view = np.lib.stride_tricks.as_strided(buf, shape=shape, strides=tuple(4 * s for s in strides) + (4,))
+    return np.array(view), buf
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_random_shape_and_layout(seed):
+    B, H, S, D, causal, pads, hpads = _case(seed)
+    G.say(f"sweep seed={seed} B={B} H={H} S={S} D={D} causal={causal} pads={pads} hpads={hpads}")
+    rng = np.random.default_rng(seed)
+    q, k, v, d_o = (rng.standard_normal((B, H, S, D)).astype(np.float32) for _ in range(4))
+    in_st, in_tot = _strided(B, H, S, D, pads[0], hpads[0])
+    out_st, out_tot = _strided(B, H, S, D, pads[1], hpads[1])
+    L = capi.lib()
+    scale = G.scale_for(D)
+    dq_, dk_, dv_ = (_upload(x, in_st, in_tot)[0] for x in (q, k, v))
+    ddo = _upload(d_o, out_st, out_tot)[0]
+    o = _upload(np.zeros_like(q), out_st, out_tot)[0]
+    lse = DeviceArray((B, H, S))
+    capi.check(L.attention_fwd(dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr, B, H, S, D, scale, int(causal),
+                               *in_st, *out_st), "attention_fwd")
+    o_np, o_buf = _download(o, out_st, (B, H, S, D))
+    lse_np = lse.numpy()
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, causal)
+    np.testing.assert_allclose(o_np, o_ref, **TOL)
+    np.testing.assert_allclose(lse_np, lse_ref, **TOL)
+    assert np.count_nonzero(o_buf == SENTINEL) == out_tot - B * H * S * D  # padding untouched
+
+    grads = [_upload(np.zeros_like(q), in_st, in_tot)[0] for _ in range(3)]
+    capi.check(L.attention_bwd(dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr, ddo.ptr,
+                               *(g.ptr for g in grads), B, H, S, D, scale, int(causal),
+                               *in_st, *out_st), "attention_bwd")
+    refs = oracle.attention_bwd(q, k, v, o_ref, lse_ref, d_o, causal)
+    for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
+        got, buf = _download(g, in_st, (B, H, S, D))
+        np.testing.assert_allclose(got, r, err_msg=name, **TOL)
+        assert np.count_nonzero(buf == SENTINEL) == in_tot - B * H * S * D, name
