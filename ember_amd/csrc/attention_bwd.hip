@@ -14,6 +14,184 @@
 // 2x slower than the VGPR form (and D = 64 causal is 6 % faster in VGPR form).
 #include "attention_bwd_kernels.h"
 
+namespace ember {
+namespace {
+
+// Short sequences (S <= 32, D <= 64): one wave per (b, h) does the whole
+// head, a single 32 x 32 block; four independent waves per workgroup, no
+// workgroup barriers, no atomics and no scratch (the row statistics are
+// formed in the kernel).
+//   S = Q K^T, dP = dO V^T                       (C[m][n]: keys on lanes)
+//   P = exp2(S*c - lse2), dS = P * (dP - delta)
+// then, 32 columns of d at a time,
+//   dV = P^T dO, dK = scale * dS^T Q             (P / dS are the A operands)
+//   dQ = scale * dS K                            (dS transposed through the
+//                                                 wave's own LDS tile)
+// Q, K, dO, V rows are read one row per lane (row = lane % 32, half of D
+// per lane half) for the S / dP products and as 32-float row segments for
+// the others; rows past S are read as row S-1 and carry P = 0.  (At
+// D = 128 the longer per-wave chain of dependent loads made this slower
+// than the workgroup kernel, which keeps D = 128 and S > 32.)
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh)
+{
+    static_assert(D <= 64, "short-sequence kernel: D <= 64");
+    constexpr int DH = D / 2;
+    constexpr int DB = D / 32;
+    constexpr int TSTR = 36;  // padded row of the 32 x 32 dS tile
+    __shared__ float tiles[kWaves][kBq * TSTR];
+    __shared__ float stats[kWaves][2][kBq];
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    const int bh = blockIdx.x * kWaves + w;
+    if (bh >= nbh) return;  // no barriers below
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
+    const float *__restrict__ qp = a.q + in_base;
+    const float *__restrict__ kp = a.k + in_base;
+    const float *__restrict__ vp = a.v + in_base;
+    const float *__restrict__ op = a.o + out_base;
+    const float *__restrict__ gp = a.dout + out_base;
+    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
+    auto clampr = [&](int r) { return r < S ? r : S - 1; };
+    float *__restrict__ st = &stats[w][0][0];
+    float *__restrict__ tile = &tiles[w][0];
+
+    // Row statistics: lane (l32, h32) holds half of row l32's <dO, O>; the
+    // halves meet across the lane halves.
+    {
+        const int rc = clampr(l32);
+        float part = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DH; c += 4) {
+            const f32x4 o4 = *(const f32x4 *)(op + rc * out_ss + h32 * DH + c);
+            const f32x4 g4 = *(const f32x4 *)(gp + rc * out_ss + h32 * DH + c);
+            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
+        }
+        part += __shfl_xor(part, 32);
+        if (h32 == 0) {
+            float l2 = INFINITY;
+            if (l32 < S) l2 = a.lse[(int64_t)bh * S + l32] * kLog2e;
+            st[l32] = l2;
+            st[kBq + l32] = l32 < S ? part : 0.0f;
+        }
+    }
+    // This wave's LDS writes land before its reads; the clobber keeps the
+    // compiler from moving memory accesses across.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+    // ---- S, dP, then P and dS ----
+    const int rr = clampr(l32);
+    f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+    for (int c = 0; c < DH; c += 4) {
+        const f32x4 q4 = *(const f32x4 *)(qp + rr * in_ss + h32 * DH + c);
+        const f32x4 k4 = *(const f32x4 *)(kp + rr * in_ss + h32 * DH + c);
+        const f32x4 g4 = *(const f32x4 *)(gp + rr * out_ss + h32 * DH + c);
+        const f32x4 v4 = *(const f32x4 *)(vp + rr * in_ss + h32 * DH + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sacc = mfma_32x32x2(q4[j], k4[j], sacc);
+            pacc = mfma_32x32x2(g4[j], v4[j], pacc);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int r0 = 8 * g + 4 * h32;  // rows r0 .. r0+3
+        const f32x4 l2 = *(const f32x4 *)&st[r0];
+        const f32x4 dl = *(const f32x4 *)&st[kBq + r0];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g + e;
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2[e]));
+            const bool vis = l32 < S && (!CAUSAL || l32 <= r0 + e);
+            p = vis ? p : 0.0f;
+            sacc[i] = p;                     // P
+            pacc[i] = p * (pacc[i] - dl[e]);  // dS
+        }
+    }
+    // dS transposed into this wave's tile: [query][key].
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tile[acc_row(i, h32) * TSTR + l32] = pacc[i];
+
+    // ---- dV, dK ----
+    // The B operands of column block db+1 are loaded before the products of
+    // block db (the scheduling barrier keeps the compiler from issuing each
+    // load just before its MFMA, which would expose one memory latency per
+    // product).
+    float gv[2][16], qv[2][16];
+    auto load_gq = [&](int db, float (&g)[16], float (&q)[16]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = clampr(acc_row(i, h32));
+            g[i] = gp[r * out_ss + 32 * db + l32];
+            q[i] = qp[r * in_ss + 32 * db + l32];
+        }
+    };
+    load_gq(0, gv[0], qv[0]);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        if (db + 1 < DB) load_gq(db + 1, gv[(db + 1) & 1], qv[(db + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x16 dv = zero16(), dk = zero16();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            dv = mfma_32x32x2(sacc[i], gv[db & 1][i], dv);
+            dk = mfma_32x32x2(pacc[i], qv[db & 1][i], dk);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int kr = acc_row(j, h32);
+            if (kr < S) {
+                a.dv[in_base + kr * in_ss + 32 * db + l32] = dv[j];
+                a.dk[in_base + kr * in_ss + 32 * db + l32] = dk[j] * a.scale;
+            }
+        }
+    }
+
+    // ---- dQ: k-step s contracts keys 16*h + s ----
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float kv[2][16];
+    auto load_k = [&](int db, float (&kk)[16]) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) kk[t] = kp[clampr(16 * h32 + t) * in_ss + 32 * db + l32];
+    };
+    load_k(0, kv[0]);
+    f32x4 a4[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) a4[s4] = *(const f32x4 *)&tile[l32 * TSTR + 16 * h32 + 4 * s4];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        if (db + 1 < DB) load_k(db + 1, kv[(db + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x16 dq = zero16();
+#pragma unroll
+        for (int t = 0; t < 16; ++t) dq = mfma_32x32x2(a4[t >> 2][t & 3], kv[db & 1][t], dq);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int row = acc_row(j, h32);
+            if (row < S) a.dq[in_base + row * in_ss + 32 * db + l32] = dq[j] * a.scale;
+        }
+    }
+}
+
+template <int D, bool CAUSAL>
+int launch_bwd_short(const BwdArgs &args, int nbh)
+{
+    const dim3 grid((unsigned)((nbh + kWaves - 1) / kWaves));
+    hipLaunchKernelGGL((attn_bwd_short<D, CAUSAL>), grid, dim3(kThreads), 0, 0, args, nbh);
+    return launch_ok("attn_bwd_short") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
+}  // namespace
+}  // namespace ember
+
 extern "C" int attention_bwd(const float *q, const float *k, const float *v, const float *o,
                              const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                              int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
@@ -26,6 +204,39 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
     int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, "attention_bwd");
     if (st != EMBER_OK || B * H * S == 0) return st;
 
+    // S <= 32 at D <= 64: one wave per head (attn_bwd_short; measured 2-3x
+    // the workgroup kernel's throughput there).
+    if (S <= kBq && D <= 64) {
+        BwdArgs sa;
+        sa.q = q;
+        sa.k = k;
+        sa.v = v;
+        sa.o = o;
+        sa.lse = lse;
+        sa.dout = d_o;
+        sa.dq = dq;
+        sa.dk = dk;
+        sa.dv = dv;
+        sa.lse2 = sa.delta = nullptr;
+        sa.H = (int)H;
+        sa.S = (int)S;
+        sa.S_pad = sa.nkb = 0;
+        sa.c = scale * kLog2e;
+        sa.scale = scale;
+        sa.in_sb = in_sb;
+        sa.in_sh = in_sh;
+        sa.in_ss = in_ss;
+        sa.out_sb = out_sb;
+        sa.out_sh = out_sh;
+        sa.out_ss = out_ss;
+        const int nbh = (int)(B * H);
+        switch (D * 2 + (causal ? 1 : 0)) {
+            case 64: return launch_bwd_short<32, false>(sa, nbh);
+            case 65: return launch_bwd_short<32, true>(sa, nbh);
+            case 128: return launch_bwd_short<64, false>(sa, nbh);
+            default: return launch_bwd_short<64, true>(sa, nbh);
+        }
+    }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
     float *stats = (float *)scratch(kScratchAttnDelta, (size_t)rows_pad * 2 * sizeof(float));
