@@ -219,9 +219,10 @@ def _timed(ev, fn, reps):
 
 
 def short_s_study(L, ev, copy_probe_mb, reps=5):
-    """The forward where it is HBM-bound: S = 32, 64, 128 at D = 128, causal,
-    2^20 query rows per tensor (the shapes `secondary` reports); achieved
-    bandwidth counts the algorithmic bytes 16*B*H*S*D + 4*B*H*S.  With
+    """Attention where it is HBM-bound: the forward at S = 32, 64, 128 and
+    D = 128, causal, 2^20 query rows per tensor (the shapes `secondary`
+    reports), achieved bandwidth over the algorithmic bytes 16*B*H*S*D +
+    4*B*H*S; then the backward at S = 32 (D = 64, 128) and S = 64 (D = 128).  With
     copy_probe_mb, one negate_tensor pass over that many MiB follows (known
     bytes for scaling the traffic counters)."""
     out = {}
@@ -242,6 +243,27 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
                                   "algorithmic_bytes": byts, "fwd_hbm_gbs": round(byts / ms / 1e6, 1),
                                   "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
         del q, k, v, o, lse
+    # The backward in the same regime: algorithmic bytes 32*B*H*S*D + 8*B*H*S
+    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 32 at D <= 64 takes
+    # the one-wave-per-head kernel.
+    for S, D in ((32, 64), (32, 128), (64, 128)):
+        B, H = (1 << 20) // S // 64, 64
+        n = B * H * S * D
+        q, k, v, g = (DeviceArray((n,), rng.standard_normal(n, dtype=np.float32)) for _ in range(4))
+        o, lse = DeviceArray((n,)), DeviceArray((B * H * S,))
+        dq, dk, dv = DeviceArray((n,)), DeviceArray((n,)), DeviceArray((n,))
+        st = capi.contiguous_strides(B, H, S, D)
+        sc = float(np.float32(1.0 / math.sqrt(D)))
+        capi.check(L.attention_fwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, B, H, S, D, sc, 1, *st, *st),
+                   "short-S forward")
+        ms = _timed(ev, lambda: L.attention_bwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, g.ptr, dq.ptr, dk.ptr,
+                                                dv.ptr, B, H, S, D, sc, 1, *st, *st), reps)
+        capi.check(what=f"short-S backward S={S} D={D}")
+        byts = 32 * n + 8 * B * H * S
+        out[f"short_s{S}_d{D}_bwd"] = {"shape": f"B{B} H{H} S{S} D{D} causal=True", "bwd_ms": round(ms, 4),
+                                       "algorithmic_bytes": byts, "bwd_hbm_gbs": round(byts / ms / 1e6, 1),
+                                       "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
+        del q, k, v, g, o, lse, dq, dk, dv
     if copy_probe_mb > 0:
         n = copy_probe_mb * (1 << 20) // 4
         src, dst = DeviceArray((n,)), DeviceArray((n,))
