@@ -314,8 +314,8 @@ def decoder_step(B, S, d, H, steps):
 def secondary(L, ev):
     """The other benchmark configurations, measured the same way (reported beside the
     headline, not part of `value`): attention fwd at configs 1 and 2, the
-    attention part of config 5 (fwd+bwd), the config-4 GEMM shapes, and the
-    forward at short S where it is HBM-bound (achieved GB/s)."""
+    attention part of config 5 (fwd+bwd), the config-4 GEMM shapes, and
+    attention at short S where it is HBM-bound (achieved GB/s)."""
     out, keep = {}, {}
     rng = np.random.default_rng(5)
 
@@ -339,7 +339,8 @@ def secondary(L, ev):
                                         dk.ptr, dv.ptr, B, H, S, D, sc, int(causal), *st, *st)
             bwd_ms = _timed(ev, b, reps)
             rec.update(bwd_ms=round(bwd_ms, 4), bwd_tflops=round(bwd_fl / bwd_ms / 1e9, 2),
-                       fwd_bwd_tflops=round((fwd_fl + bwd_fl) / (fwd_ms + bwd_ms) / 1e9, 2))
+                       fwd_bwd_tflops=round((fwd_fl + bwd_fl) / (fwd_ms + bwd_ms) / 1e9, 2),
+                       bwd_hbm_gbs=round((32 * n + 8 * B * H * S) / bwd_ms / 1e6, 1))
         fwd_bytes = 16 * B * H * S * D + 4 * B * H * S
         rec["fwd_hbm_gbs"] = round(fwd_bytes / fwd_ms / 1e6, 1)
         capi.check(what=tag)
@@ -352,6 +353,8 @@ def secondary(L, ev):
     attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20)
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
+    # The backward where it is HBM-bound (one wave per head at S <= 32, D <= 64).
+    attn("short_s32_d64_fwd_bwd", (1 << 20) // 32 // 64, 64, 32, 64, True, True, 20)
 
     # Fused Adam over config 5's parameters (pre-LN decoder block, d=1024,
     # MLP 4x): LN gains/biases, QKV, out-proj, MLP weights and biases.
