@@ -1,5 +1,6 @@
 // attention_bwd.hip -- entry point of the fused flash-attention backward
-// (fp32, gfx950); the kernels are in attention_bwd_kernels.h.
+// (fp32, gfx950); the workgroup kernels are in attention_bwd_kernels.h, the
+// one-wave-per-head kernel for S <= 32, D <= 64 is below.
 //
 // No reference counterpart (pawel002/ember has no attention): the operator is
 // new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
