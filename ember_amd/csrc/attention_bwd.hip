@@ -1,6 +1,6 @@
 // attention_bwd.hip -- entry point of the fused flash-attention backward
 // (fp32, gfx950); the workgroup kernels are in attention_bwd_kernels.h, the
-// one-wave-per-head kernel for S <= 32, D <= 64 is below.
+// short-sequence kernel (S <= 32, one or two waves per head) is below.
 //
 // No reference counterpart (pawel002/ember has no attention): the operator is
 // new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
@@ -18,10 +18,10 @@
 namespace ember {
 namespace {
 
-// Short sequences (S <= 32, D <= 64): one wave per (b, h) does the whole
-// head, a single 32 x 32 block; four independent waves per workgroup, no
-// workgroup barriers, no atomics and no scratch (the row statistics are
-// formed in the kernel).
+// Short sequences (S <= 32): WPH waves per (b, h) (1, or 2 at D = 128) do
+// the whole head, a single 32 x 32 block; four independent waves per
+// workgroup, no workgroup barriers, no atomics and no scratch (the row
+// statistics are formed in the kernel).
 //   S = Q K^T, dP = dO V^T                       (C[m][n]: keys on lanes)
 //   P = exp2(S*c - lse2), dS = P * (dP - delta)
 // then, 32 columns of d at a time,
@@ -30,13 +30,14 @@ namespace {
 //                                                 wave's own LDS tile)
 // Q, K, dO, V rows are read one row per lane (row = lane % 32, half of D
 // per lane half) for the S / dP products and as 32-float row segments for
-// the others; rows past S are read as row S-1 and carry P = 0.  (At
-// D = 128 the longer per-wave chain of dependent loads made this slower
-// than the workgroup kernel, which keeps D = 128 and S > 32.)
-template <int D, bool CAUSAL>
+// the others; rows past S are read as row S-1 and carry P = 0.  With two
+// waves per head both form S, dP, P and dS and each writes half of the
+// columns of dV, dK and dQ, which halves the per-wave chain of dependent
+// loads (one wave per head at D = 128 was slower than the workgroup kernel).
+template <int D, bool CAUSAL, int WPH>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh)
 {
-    static_assert(D <= 64, "short-sequence kernel: D <= 64");
+    static_assert(WPH == 1 || (WPH == 2 && D >= 64), "waves per head");
     constexpr int DH = D / 2;
     constexpr int DB = D / 32;
     constexpr int TSTR = 36;  // padded row of the 32 x 32 dS tile
@@ -47,8 +48,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
-    const int bh = blockIdx.x * kWaves + w;
+    const int bh = (blockIdx.x * kWaves + w) / WPH;
     if (bh >= nbh) return;  // no barriers below
+    const int db0 = WPH == 1 ? 0 : (w & 1) * (DB / 2);
+    constexpr int NDB = DB / WPH;
     const int b = bh / a.H;
     const int hh = bh - b * a.H;
     const int S = a.S;
@@ -135,16 +138,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh
             q[i] = qp[r * in_ss + 32 * db + l32];
         }
     };
-    load_gq(0, gv[0], qv[0]);
+    load_gq(db0, gv[0], qv[0]);
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        if (db + 1 < DB) load_gq(db + 1, gv[(db + 1) & 1], qv[(db + 1) & 1]);
+    for (int e = 0; e < NDB; ++e) {
+        const int db = db0 + e;
+        if (e + 1 < NDB) load_gq(db + 1, gv[(e + 1) & 1], qv[(e + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
         f32x16 dv = zero16(), dk = zero16();
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            dv = mfma_32x32x2(sacc[i], gv[db & 1][i], dv);
-            dk = mfma_32x32x2(pacc[i], qv[db & 1][i], dk);
+            dv = mfma_32x32x2(sacc[i], gv[e & 1][i], dv);
+            dk = mfma_32x32x2(pacc[i], qv[e & 1][i], dk);
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -163,17 +167,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh
 #pragma unroll
         for (int t = 0; t < 16; ++t) kk[t] = kp[clampr(16 * h32 + t) * in_ss + 32 * db + l32];
     };
-    load_k(0, kv[0]);
+    load_k(db0, kv[0]);
     f32x4 a4[4];
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) a4[s4] = *(const f32x4 *)&tile[l32 * TSTR + 16 * h32 + 4 * s4];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        if (db + 1 < DB) load_k(db + 1, kv[(db + 1) & 1]);
+    for (int e = 0; e < NDB; ++e) {
+        const int db = db0 + e;
+        if (e + 1 < NDB) load_k(db + 1, kv[(e + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
         f32x16 dq = zero16();
 #pragma unroll
-        for (int t = 0; t < 16; ++t) dq = mfma_32x32x2(a4[t >> 2][t & 3], kv[db & 1][t], dq);
+        for (int t = 0; t < 16; ++t) dq = mfma_32x32x2(a4[t >> 2][t & 3], kv[e & 1][t], dq);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const int row = acc_row(j, h32);
@@ -185,8 +190,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh
 template <int D, bool CAUSAL>
 int launch_bwd_short(const BwdArgs &args, int nbh)
 {
-    const dim3 grid((unsigned)((nbh + kWaves - 1) / kWaves));
-    hipLaunchKernelGGL((attn_bwd_short<D, CAUSAL>), grid, dim3(kThreads), 0, 0, args, nbh);
+    // Two waves per head at D = 128 (1.6 -> 2.4 TB/s at S = 32: half the
+    // chain of dependent loads per wave); one at D <= 64 (two measured 2.3
+    // against 3.3 TB/s there).
+    constexpr int WPH = D == 128 ? 2 : 1;
+    const dim3 grid((unsigned)(((int64_t)nbh * WPH + kWaves - 1) / kWaves));
+    hipLaunchKernelGGL((attn_bwd_short<D, CAUSAL, WPH>), grid, dim3(kThreads), 0, 0, args, nbh);
     return launch_ok("attn_bwd_short") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
@@ -205,9 +214,9 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
     int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, "attention_bwd");
     if (st != EMBER_OK || B * H * S == 0) return st;
 
-    // S <= 32 at D <= 64: one wave per head (attn_bwd_short; measured 2-3x
+    // S <= 32: one or two waves per head (attn_bwd_short; measured 1.5-3x
     // the workgroup kernel's throughput there).
-    if (S <= kBq && D <= 64) {
+    if (S <= kBq) {
         BwdArgs sa;
         sa.q = q;
         sa.k = k;
@@ -235,7 +244,9 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
             case 64: return launch_bwd_short<32, false>(sa, nbh);
             case 65: return launch_bwd_short<32, true>(sa, nbh);
             case 128: return launch_bwd_short<64, false>(sa, nbh);
-            default: return launch_bwd_short<64, true>(sa, nbh);
+            case 129: return launch_bwd_short<64, true>(sa, nbh);
+            case 256: return launch_bwd_short<128, false>(sa, nbh);
+            default: return launch_bwd_short<128, true>(sa, nbh);
         }
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;

@@ -135,7 +135,7 @@ int attention_fwd(const float *q, const float *k, const float *v, float *o, floa
  * upstream gradient d_o, writes dq, dk, dv (same layout as q, k, v).  P is
  * recomputed from lse; the S x S matrix is never stored.  Needs
  * 2*B*H*S_pad*4 bytes of device scratch (S_pad = S rounded up to 32; none at
- * S <= 32 with D <= 64), which the library keeps cached between calls. */
+ * S <= 32), which the library keeps cached between calls. */
 int attention_bwd(const float *q, const float *k, const float *v, const float *o,
                   const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                   int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
