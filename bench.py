@@ -244,8 +244,8 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
                                   "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
         del q, k, v, o, lse
     # The backward in the same regime: algorithmic bytes 32*B*H*S*D + 8*B*H*S
-    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 32 at D <= 64 takes
-    # the one-wave-per-head kernel.
+    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 32 takes the
+    # short-sequence kernel (one wave per head, two at D = 128).
     for S, D in ((32, 64), (32, 128), (64, 128)):
         B, H = (1 << 20) // S // 64, 64
         n = B * H * S * D
@@ -353,8 +353,9 @@ def secondary(L, ev):
     attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20)
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
-    # The backward where it is HBM-bound (one wave per head at S <= 32, D <= 64).
+    # The backward where it is HBM-bound (S <= 32: one wave per head, two at D = 128).
     attn("short_s32_d64_fwd_bwd", (1 << 20) // 32 // 64, 64, 32, 64, True, True, 20)
+    attn("short_s32_d128_fwd_bwd", (1 << 20) // 32 // 64, 64, 32, 128, True, True, 20)
 
     # Fused Adam over config 5's parameters (pre-LN decoder block, d=1024,
     # MLP 4x): LN gains/biases, QKV, out-proj, MLP weights and biases.
