@@ -1,6 +1,7 @@
 // attention_bwd.hip -- entry point of the fused flash-attention backward
 // (fp32, gfx950); the workgroup kernels are in attention_bwd_kernels.h, the
-// short-sequence kernel (S <= 32, one or two waves per head) is below.
+// short-sequence kernels (S <= 32: one or two waves per head; 32 < S <= 64
+// at D <= 64: one wave per key block) are below.
 //
 // No reference counterpart (pawel002/ember has no attention): the operator is
 // new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
@@ -187,6 +188,159 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh
     }
 }
 
+// 32 < S <= 64 (D <= 64): one wave per (b, h, key block kb) takes the pairs
+// (qb, kb), qb from kb (causal) or 0 to 1, with the row statistics from
+// attn_bwd_pre's scratch.  dV and dK of the
+// wave's key block are summed over its pairs in registers and stored; dQ of
+// each pair's query block is added with atomics (attn_bwd_pre zeroed it), as
+// the two key blocks' waves both contribute.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_short2(BwdArgs a, int nbh)
+{
+    static_assert(D <= 64, "S <= 64 kernel: D <= 64");
+    constexpr int DH = D / 2;
+    constexpr int DB = D / 32;
+    constexpr int TSTR = 36;  // padded row of a 32 x 32 dS tile
+    __shared__ float tiles[kWaves][2][kBq * TSTR];
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h32 = lane >> 5;
+    const int l32 = lane & 31;
+    const int item = blockIdx.x * kWaves + w;
+    const int bh = item / 2;
+    if (bh >= nbh) return;  // no barriers below
+    const int kb = item & 1;
+    const int qlo = CAUSAL ? kb : 0;  // pairs (qlo .. 1, kb)
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
+    const float *__restrict__ qp = a.q + in_base;
+    const float *__restrict__ kp = a.k + in_base;
+    const float *__restrict__ vp = a.v + in_base;
+    const float *__restrict__ gp = a.dout + out_base;
+    const float *__restrict__ l2p = a.lse2 + (int64_t)bh * a.S_pad;  // S_pad = 64
+    const float *__restrict__ dlp = a.delta + (int64_t)bh * a.S_pad;
+    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
+    auto clampr = [&](int r) { return r < S ? r : S - 1; };
+
+    // ---- S, dP, P and dS of each pair ----
+    f32x16 pp[2], dd[2];
+    const int key = kBq * kb + l32;
+    const int rk = clampr(key);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int qb = qlo + j;
+        if (qb > 1) break;
+        const int rq = clampr(kBq * qb + l32);
+        f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+        for (int c = 0; c < DH; c += 4) {
+            const f32x4 q4 = *(const f32x4 *)(qp + rq * in_ss + h32 * DH + c);
+            const f32x4 k4 = *(const f32x4 *)(kp + rk * in_ss + h32 * DH + c);
+            const f32x4 g4 = *(const f32x4 *)(gp + rq * out_ss + h32 * DH + c);
+            const f32x4 v4 = *(const f32x4 *)(vp + rk * in_ss + h32 * DH + c);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                sacc = mfma_32x32x2(q4[t], k4[t], sacc);
+                pacc = mfma_32x32x2(g4[t], v4[t], pacc);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int r0 = kBq * qb + 8 * g + 4 * h32;  // rows r0 .. r0+3 (< S_pad)
+            const f32x4 l2 = *(const f32x4 *)(l2p + r0);
+            const f32x4 dl = *(const f32x4 *)(dlp + r0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = 4 * g + e;
+                float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2[e]));
+                const bool vis = key < S && (!CAUSAL || key <= r0 + e);
+                p = vis ? p : 0.0f;
+                sacc[i] = p;
+                pacc[i] = p * (pacc[i] - dl[e]);
+            }
+        }
+        pp[j] = sacc;
+        dd[j] = pacc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tiles[w][j][acc_row(i, h32) * TSTR + l32] = pacc[i];
+    }
+
+    // ---- dV, dK of key block kb over the pairs ----
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        f32x16 dv = zero16(), dk = zero16();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int qb = qlo + j;
+            if (qb > 1) break;
+            float gv[16], qv[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = clampr(kBq * qb + acc_row(i, h32));
+                gv[i] = gp[r * out_ss + 32 * db + l32];
+                qv[i] = qp[r * in_ss + 32 * db + l32];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                dv = mfma_32x32x2(pp[j][i], gv[i], dv);
+                dk = mfma_32x32x2(dd[j][i], qv[i], dk);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int kr = kBq * kb + acc_row(t, h32);
+            if (kr < S) {
+                a.dv[in_base + kr * in_ss + 32 * db + l32] = dv[t];
+                a.dk[in_base + kr * in_ss + 32 * db + l32] = dk[t] * a.scale;
+            }
+        }
+    }
+
+    // ---- dQ of each pair's query block: dS (through LDS) times K[kb] ----
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        float kv[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) kv[t] = kp[clampr(kBq * kb + 16 * h32 + t) * in_ss + 32 * db + l32];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int qb = qlo + j;
+            if (qb > 1) break;
+            f32x16 dq = zero16();
+#pragma unroll
+            for (int s4 = 0; s4 < 16; s4 += 4) {
+                const f32x4 a4 = *(const f32x4 *)&tiles[w][j][l32 * TSTR + 16 * h32 + s4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) dq = mfma_32x32x2(a4[t], kv[s4 + t], dq);
+            }
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int row = kBq * qb + acc_row(t, h32);
+                if (row < S) unsafeAtomicAdd(a.dq + in_base + (int64_t)row * in_ss + 32 * db + l32, dq[t] * a.scale);
+            }
+        }
+    }
+}
+
+template <int D, bool CAUSAL>
+int launch_bwd_short2(const BwdArgs &args, int64_t rows_pad, int nbh)
+{
+    constexpr int RPB = 256 / (D / 4);
+    const int pre_blocks = (int)((rows_pad + RPB - 1) / RPB);
+    hipLaunchKernelGGL((attn_bwd_pre<D>), dim3(pre_blocks), dim3(256), 0, 0, args, rows_pad);
+    if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
+    const dim3 grid((unsigned)(((int64_t)nbh * 2 + kWaves - 1) / kWaves));
+    hipLaunchKernelGGL((attn_bwd_short2<D, CAUSAL>), grid, dim3(kThreads), 0, 0, args, nbh);
+    return launch_ok("attn_bwd_short2") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
 template <int D, bool CAUSAL>
 int launch_bwd_short(const BwdArgs &args, int nbh)
 {
@@ -279,6 +433,17 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
     args.out_sh = out_sh;
     args.out_ss = out_ss;
     const int nblocks = args.nkb * (int)(B * H);
+    // 32 < S <= 64 at D <= 64: one wave per (head, key block) (measured
+    // +2 to +58 % over the workgroup kernel; at D = 128, two waves per key
+    // block measured -17 to +17 %, so D = 128 stays with the workgroup kernel).
+    if (S <= 2 * kBq && D <= 64) {
+        switch (D * 2 + (causal ? 1 : 0)) {
+            case 64: return launch_bwd_short2<32, false>(args, rows_pad, (int)(B * H));
+            case 65: return launch_bwd_short2<32, true>(args, rows_pad, (int)(B * H));
+            case 128: return launch_bwd_short2<64, false>(args, rows_pad, (int)(B * H));
+            default: return launch_bwd_short2<64, true>(args, rows_pad, (int)(B * H));
+        }
+    }
     switch (D * 2 + (causal ? 1 : 0)) {
         case 64: return launch_bwd<32, false>(args, rows_pad, nblocks);
         case 65: return launch_bwd<32, true>(args, rows_pad, nblocks);
