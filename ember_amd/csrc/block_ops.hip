@@ -83,8 +83,31 @@ __global__ __launch_bounds__(256) void col_sum_partial(const float *__restrict__
 
 // out[y][c] = sum over rows r in [y*rpw, (y+1)*rpw) of x[r][c], c in quads.
 constexpr int kQuads = 16, kGroups = 16, kSliceRows = 256;
-__global__ __launch_bounds__(256) void col_reduce4(const float *__restrict__ x, float *__restrict__ out,
-                                                   int64_t rows, int cols, int rpw)
+// Row loaders for col_reduce4: a plain matrix, or the GELU backward
+// evaluated on the fly (dx stored as it is summed, the same bits as
+// gelu_bwd_vec4 with the output recomputed).
+struct PlainRows {
+    const float *x;
+    __device__ __forceinline__ float4 operator()(int64_t off) const { return *(const float4 *)(x + off); }
+};
+struct GeluBwdRows {
+    const float *dy, *u;
+    float *dx;
+    __device__ __forceinline__ float4 operator()(int64_t off) const
+    {
+        const f32x4 g = *(const f32x4 *)(dy + off);
+        const f32x4 x = *(const f32x4 *)(u + off);
+        f32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = gelu_bwd_one<true>(g[j], x[j], 0.0f);
+        *(f32x4 *)(dx + off) = o;
+        return make_float4(o[0], o[1], o[2], o[3]);
+    }
+};
+
+template <class LD>
+__global__ __launch_bounds__(256) void col_reduce4(LD ld, float *__restrict__ out, int64_t rows, int cols,
+                                                   int rpw)
 {
     __shared__ float4 red[kGroups][kQuads];
     const int q = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
@@ -99,7 +122,7 @@ __global__ __launch_bounds__(256) void col_reduce4(const float *__restrict__ x, 
         for (; r + 7 * kGroups < r1; r += 8 * kGroups) {
             float4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = *(const float4 *)(x + (r + u * kGroups) * cols + 4 * quad);
+            for (int u = 0; u < 8; ++u) v[u] = ld((r + u * kGroups) * cols + 4 * quad);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 s.x += v[u].x;
@@ -109,7 +132,7 @@ __global__ __launch_bounds__(256) void col_reduce4(const float *__restrict__ x, 
             }
         }
         for (; r < r1; r += kGroups) {
-            const float4 v = *(const float4 *)(x + r * cols + 4 * quad);
+            const float4 v = ld(r * cols + 4 * quad);
             s.x += v.x;
             s.y += v.y;
             s.z += v.z;
@@ -140,6 +163,30 @@ __global__ __launch_bounds__(256) void col_sum_final(const float *__restrict__ p
     float s = 0.0f;
     for (int k = 0; k < slices; ++k) s += part[(int64_t)k * cols + c];
     out[c] = s;
+}
+
+// Column sums of a rows x cols matrix (cols % 4 == 0) read through ld: one
+// pass when it fits one 256-row slice, else slice partials in scratch and a
+// second pass over them in slice order.
+template <class LD>
+int col_sum4(LD ld, float *out, int64_t rows, int64_t cols)
+{
+    const unsigned cblocks = (unsigned)((cols / 4 + kQuads - 1) / kQuads);
+    const int64_t slices4 = (rows + kSliceRows - 1) / kSliceRows;
+    if (slices4 > 65535) return record_error(EMBER_ERR_UNSUPPORTED, "col_sum");
+    if (slices4 == 1) {
+        hipLaunchKernelGGL((col_reduce4<LD>), dim3(cblocks, 1), dim3(256), 0, 0, ld, out, rows, (int)cols,
+                           (int)rows);
+        return launch_ok("col_reduce4") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
+    float *part4 = (float *)scratch(kScratchColSum, (size_t)slices4 * cols * sizeof(float));
+    if (!part4) return EMBER_ERR_OUT_OF_MEMORY;
+    hipLaunchKernelGGL((col_reduce4<LD>), dim3(cblocks, (unsigned)slices4), dim3(256), 0, 0, ld, part4, rows,
+                       (int)cols, kSliceRows);
+    if (!launch_ok("col_reduce4")) return EMBER_ERR_DEVICE;
+    hipLaunchKernelGGL((col_reduce4<PlainRows>), dim3(cblocks, 1), dim3(256), 0, 0, PlainRows{part4}, out,
+                       slices4, (int)cols, (int)slices4);
+    return launch_ok("col_reduce4") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 }  // namespace
@@ -173,24 +220,8 @@ extern "C" int col_sum(const float *x, float *out, int64_t rows, int64_t cols)
     if (rows < 0 || cols < 0 || cols > INT32_MAX) return record_error(EMBER_ERR_INVALID_ARGUMENT, "col_sum");
     if (cols == 0) return EMBER_OK;
     if (!out || (rows > 0 && !x)) return record_error(EMBER_ERR_INVALID_ARGUMENT, "col_sum");
-    if (rows > 0 && cols % 4 == 0 && (((uintptr_t)x | (uintptr_t)out) % 16) == 0) {
-        const unsigned cblocks = (unsigned)((cols / 4 + kQuads - 1) / kQuads);
-        const int64_t slices4 = (rows + kSliceRows - 1) / kSliceRows;
-        if (slices4 > 65535) return record_error(EMBER_ERR_UNSUPPORTED, "col_sum");
-        if (slices4 == 1) {
-            hipLaunchKernelGGL(col_reduce4, dim3(cblocks, 1), dim3(256), 0, 0, x, out, rows, (int)cols,
-                               (int)rows);
-            return launch_ok("col_reduce4") ? EMBER_OK : EMBER_ERR_DEVICE;
-        }
-        float *part4 = (float *)scratch(kScratchColSum, (size_t)slices4 * cols * sizeof(float));
-        if (!part4) return EMBER_ERR_OUT_OF_MEMORY;
-        hipLaunchKernelGGL(col_reduce4, dim3(cblocks, (unsigned)slices4), dim3(256), 0, 0, x, part4,
-                           rows, (int)cols, kSliceRows);
-        if (!launch_ok("col_reduce4")) return EMBER_ERR_DEVICE;
-        hipLaunchKernelGGL(col_reduce4, dim3(cblocks, 1), dim3(256), 0, 0, (const float *)part4, out,
-                           slices4, (int)cols, (int)slices4);
-        return launch_ok("col_reduce4") ? EMBER_OK : EMBER_ERR_DEVICE;
-    }
+    if (rows > 0 && cols % 4 == 0 && (((uintptr_t)x | (uintptr_t)out) % 16) == 0)
+        return col_sum4(PlainRows{x}, out, rows, cols);
     const int64_t slices = (rows + kRowsPerSlice - 1) / kRowsPerSlice;
     if (slices > 65535) return record_error(EMBER_ERR_UNSUPPORTED, "col_sum");
     float *part = nullptr;
@@ -204,4 +235,20 @@ extern "C" int col_sum(const float *x, float *out, int64_t rows, int64_t cols)
     hipLaunchKernelGGL(col_sum_final, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, 0,
                        (const float *)part, out, (int)slices, (int)cols);
     return launch_ok("col_sum_final") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
+extern "C" int gelu_bwd_col_sum(const float *dy, const float *u, float *dx, float *dbias, int64_t rows,
+                                int64_t cols)
+{
+    using namespace ember;
+    if (rows < 0 || cols < 0 || cols > INT32_MAX || rows > INT64_MAX / (cols > 0 ? cols : 1))
+        return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd_col_sum");
+    if (cols == 0) return EMBER_OK;
+    if (!dbias || (rows > 0 && (!dy || !u || !dx))) return record_error(EMBER_ERR_INVALID_ARGUMENT, "gelu_bwd_col_sum");
+    // One pass (dx written while its columns are summed) for 16-byte aligned
+    // rows; otherwise the two entry points in turn (the same results).
+    if (rows > 0 && cols % 4 == 0 && (((uintptr_t)dy | (uintptr_t)u | (uintptr_t)dx | (uintptr_t)dbias) % 16) == 0)
+        return col_sum4(GeluBwdRows{dy, u, dx}, dbias, rows, cols);
+    const int st = gelu_bwd(dy, u, nullptr, dx, rows * cols);
+    return st != EMBER_OK ? st : col_sum(dx, dbias, rows, cols);
 }

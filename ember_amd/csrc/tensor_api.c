@@ -811,6 +811,34 @@ static PyObject *py_col_sum(PyObject *module, PyObject *args)
     return (PyObject *)out;
 }
 
+/* _gelu_bwd_col_sum(dy, u, rows, cols) -> (dx, dbias): _gelu_bwd (output
+ * recomputed) and _col_sum of its result in one pass, the same bits. */
+static PyObject *py_gelu_bwd_col_sum(PyObject *module, PyObject *args)
+{
+    TensorObject *dy, *u;
+    long long rows, cols;
+    (void)module;
+    if (!PyArg_ParseTuple(args, "O!O!LL", &TensorType, &dy, &TensorType, &u, &rows, &cols)) return NULL;
+    if (rows < 0 || cols < 0 || dy->size != u->size || u->size != (Py_ssize_t)(rows * cols)) {
+        PyErr_SetString(PyExc_ValueError, "_gelu_bwd_col_sum: size mismatch");
+        return NULL;
+    }
+    TensorObject *dx = alloc_tensor(u->size);
+    if (!dx) return NULL;
+    TensorObject *db = alloc_tensor((Py_ssize_t)cols);
+    if (!db) {
+        Py_DECREF(dx);
+        return NULL;
+    }
+    int st = gelu_bwd_col_sum(dy->d_ptr, u->d_ptr, dx->d_ptr, db->d_ptr, rows, cols);
+    if (raise_status(st, "_gelu_bwd_col_sum")) {
+        Py_DECREF(dx);
+        Py_DECREF(db);
+        return NULL;
+    }
+    return Py_BuildValue("(NN)", dx, db);
+}
+
 static PyObject *py_layernorm_fwd(PyObject *module, PyObject *args)
 {
     TensorObject *x, *g, *b;
@@ -1047,6 +1075,7 @@ static PyMethodDef module_methods[] = {
     METHOD("_gemm", py_gemm, "op(a) @ op(b) + bias + residual with either operand transposed in place"),
     METHOD("_gelu_bwd", py_gelu_bwd, "backward of Ember's GELU"),
     METHOD("_col_sum", py_col_sum, "column sums (bias gradient)"),
+    METHOD("_gelu_bwd_col_sum", py_gelu_bwd_col_sum, "GELU backward and its column sums in one pass"),
     METHOD("_layernorm_fwd", py_layernorm_fwd, "LayerNorm -> (y, mean, rstd)"),
     METHOD("_layernorm_bwd", py_layernorm_bwd, "LayerNorm backward -> (dx, dgamma, dbeta)"),
     METHOD("_attention_fwd_packed", py_attention_fwd_packed, "attention on packed (B,S,3,H,D) qkv"),

@@ -195,10 +195,15 @@ class Linear(Layer):
             raise RuntimeError("forward() must run before backward()")
         if self.activation == "gelu":
             # The GELU output is recomputed from the pre-activation in the
-            # kernel (bit-identical to the forward's).
-            grad_y = Tensor._from_core(C._gelu_bwd(grad_y._core, self.pre._core), grad_y.shape)
+            # kernel (bit-identical to the forward's); the bias gradient is
+            # summed in the same pass.
+            n, m = _rows(grad_y)
+            g_core, b_core = C._gelu_bwd_col_sum(grad_y._core, self.pre._core, n, m)
+            grad_y = Tensor._from_core(g_core, grad_y.shape)
+            self.grad_b = Tensor._from_core(b_core, (m,))
+        else:
+            self.grad_b = col_sum(grad_y)
         self.grad_w = weight_grad(self.x, grad_y)
-        self.grad_b = col_sum(grad_y)
         return input_grad(grad_y, self.w)
 
 
@@ -337,8 +342,10 @@ class DecoderBlock(Layer):
         # MLP: y = x2 + GELU(h2 W1 + b1) W2 + b2
         g_w2, g_b2 = weight_grad(a, grad_y), col_sum(grad_y)
         da = input_grad(grad_y, self.w_2)
-        du = Tensor._from_core(C._gelu_bwd(da._core, u._core), da.shape)  # a recomputed from u
-        g_w1, g_b1 = weight_grad(h2, du), col_sum(du)
+        n, m = _rows(da)
+        du_core, g_b1_core = C._gelu_bwd_col_sum(da._core, u._core, n, m)  # a recomputed from u
+        du, g_b1 = Tensor._from_core(du_core, da.shape), Tensor._from_core(g_b1_core, (m,))
+        g_w1 = weight_grad(h2, du)
         dx2 = self.ln2.backward(input_grad(du, self.w_1), residual=grad_y)
         # attention: x2 = x + O Wo + bo
         g_wo, g_bo = weight_grad(o, dx2), col_sum(dx2)

@@ -198,6 +198,13 @@ int gelu_bwd(const float *dy, const float *u, const float *y, float *dx, int64_t
  * (fixed summation order); uses library scratch. */
 int col_sum(const float *x, float *out, int64_t rows, int64_t cols);
 
+/* dx = gelu_bwd(dy, u) (output recomputed) and dbias = col_sum(dx) in one
+ * pass: the same bits as the two calls in turn, without re-reading dx.
+ * Replaces GELU.backward followed by em.sum(grad_y, axis=0) in a Linear
+ * layer with a GELU activation (ember/nn/activations.py:61-66,
+ * ember/nn/layers.py:54).  Uses library scratch. */
+int gelu_bwd_col_sum(const float *dy, const float *u, float *dx, float *dbias, int64_t rows, int64_t cols);
+
 /* LayerNorm over the last dimension d (d % 4 == 0, d <= 4096; all pointers
  * 16-byte aligned and non-NULL):
  *   mean = sum(x)/d, var = sum((x-mean)^2)/d, rstd = 1/sqrt(var + eps),

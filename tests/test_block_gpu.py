@@ -81,6 +81,23 @@ def test_gelu_bwd_and_col_sum():
         np.testing.assert_allclose(got.to_np(), x.astype(np.float64).sum(0), rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (300, 1024), (257, 12), (256, 64), (5, 7), (1, 4)])
+def test_gelu_bwd_col_sum_is_bitwise_the_two_calls(rows, cols):
+    """_gelu_bwd_col_sum (one pass, dx summed as it is written) gives the
+    same bits as _gelu_bwd followed by _col_sum: one 256-row slice, several
+    slices, and an unaligned width (the two entry points in turn)."""
+    G.say(f"gelu_bwd_col_sum rows={rows} cols={cols}")
+    u, dy = rnd((rows, cols), 17, 3.0), rnd((rows, cols), 18)
+    tu, tdy = Tensor(u), Tensor(dy)
+    dx, db = _core._gelu_bwd_col_sum(tdy._core, tu._core, rows, cols)
+    dx_ref = _core._gelu_bwd(tdy._core, tu._core)
+    db_ref = _core._col_sum(dx_ref, rows, cols)
+    assert np.array_equal(dx._to_np(), dx_ref._to_np())
+    assert np.array_equal(db._to_np(), db_ref._to_np())
+    np.testing.assert_allclose(db._to_np(), dx_ref._to_np().reshape(rows, cols).astype(np.float64).sum(0),
+                               rtol=1e-5, atol=1e-4)
+
+
 @pytest.mark.parametrize("n", [4096 * 33, 5001])
 def test_gelu_bwd_recomputed_output_is_bitwise_the_stored_one(n):
     """_gelu_bwd(dy, u) recomputes the GELU output from u: bit-identical to
