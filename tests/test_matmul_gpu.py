@@ -114,6 +114,25 @@ def test_gemm_ex_batched_split(ta, tb):
         _check(got[i], a[i], b[i])
 
 
+@pytest.mark.parametrize("n,k,m,ta,tb,batch",
+                         [(8192, 1024, 1024, False, False, 1), (8192, 4096, 1024, False, True, 1),
+                          (1024, 512, 512, True, False, 1), (512, 96, 256, True, True, 2),
+                          (256, 64, 768, False, False, 3)])
+def test_gemm_two_k_groups(n, k, m, ta, tb, batch):
+    """Outputs with no more 128 x 256 tiles than CUs and an even slab count
+    take the kernel whose workgroup splits the k-slabs between two wave
+    groups (even / odd slabs, summed through LDS): config 5's 8192 x 1024
+    products, transposed operands, batches, and a 4-slab minimum."""
+    a, b = _u((batch, n, k), n + k), _u((batch, k, m), m + 2)
+    sa = np.stack([_stored(a[i], ta) for i in range(batch)])
+    sb = np.stack([_stored(b[i], tb) for i in range(batch)])
+    got = G.gemm_ex(sa if batch > 1 else sa[0], sb if batch > 1 else sb[0], ta, tb)
+    got = got.reshape(batch, n, m)
+    rows = np.random.default_rng(n).choice(n, min(n, 64), replace=False)
+    for i in range(batch):
+        _check(got[i][rows], a[i][rows], b[i])
+
+
 @pytest.mark.parametrize("n,k,m", [(128, 4096, 256), (256, 64, 512), (70, 40, 30)])
 def test_gemm_ex_epilogue_with_and_without_split(n, k, m):
     """bias + residual, and bias + GELU with pre, through the split-K reduction
