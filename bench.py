@@ -166,6 +166,33 @@ def cpu_other_configs(threads, keep):
     return out
 
 
+def host_info(threads):
+    """Where the CPU baseline ran: the host's CPU model and logical CPU count,
+    the CPUs this process may use, and the worker threads actually used."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = None
+    return {
+        "cpu_model": model,
+        "host_cores": os.cpu_count(),
+        "affinity_cores": allowed,
+        "threads": threads,
+        "thread_cap": "threads = min(16, os.cpu_count()): a GPU box allots 16 host CPUs to its one GPU's "
+                      "jobs, so an all-cores pool of os.cpu_count() workers is not run; the reference's "
+                      "CPU ops are single-threaded C, one head (or row block) per thread",
+    }
+
+
 def cpu_baseline(S, D, threads, inputs, outputs):
     """Times Ember's CPU path on `threads` heads of the timed workload (batch
     0, heads 0..threads-1, one per thread), fwd+bwd, and compares its
@@ -596,6 +623,7 @@ def main(argv=None):
         cpu_heads = min(threads, H)
         gpu_out = [x.numpy()[:1, :cpu_heads] for x in (o, dq, dk, dv)]
         result["cpu_baseline"] = cpu_baseline(S, D, cpu_heads, [x[:1, :cpu_heads] for x in host], gpu_out)
+        result["cpu_baseline"].update(host_info(cpu_heads))
         others = cpu_other_configs(threads, keep)
         if others is not None:
             result["cpu_baseline"]["other_configs"] = others

@@ -41,6 +41,7 @@ HIP_SOURCES = [
     ("layernorm.hip", []),
     ("block_ops.hip", []),
     ("softmax.hip", []),
+    ("distributions.hip", []),
 ]
 
 HIP_FLAGS = [

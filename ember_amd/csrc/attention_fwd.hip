@@ -116,21 +116,22 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
     const float *__restrict__ vbase = a.v + in_base;
 
     // Byte offsets of this wave's copy slots within a tile (slot s is copy
-    // t = w + 4s, chunk p = 64t + lane).  Offsets stay below
-    // 64 * in_ss * 4 < 2^32.
-    int koff[T::KSL];
+    // t = w + 4s, chunk p = 64t + lane).  The element offset r * in_ss + 4c
+    // (r < 64, in_ss < 2^24) fits an int; the byte offset, up to
+    // 4 * 63 * 2^24 + 4 * D, only fits 32 bits unsigned.
+    unsigned koff[T::KSL];
 #pragma unroll
     for (int s = 0; s < T::KSL; ++s) {
         const int p = 64 * (w + kWaves * s) + lane;
         const int r = p / T::KCH, c = p - r * T::KCH;
-        koff[s] = c < D / 4 ? 4 * (r * in_ss + 4 * c) : 0;
+        koff[s] = c < D / 4 ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
     }
-    int voff[kVoffRegs ? T::VSL : 1];
+    unsigned voff[kVoffRegs ? T::VSL : 1];
 #pragma unroll
     for (int s = 0; s < (kVoffRegs ? T::VSL : 1); ++s) {
         const int p = 64 * (w + kWaves * s) + lane;
         const int r = p / (D / 4), c = p - r * (D / 4);
-        voff[s] = 4 * (r * in_ss + 4 * c);
+        voff[s] = 4u * (unsigned)(r * in_ss + 4 * c);
     }
 
     // Rows past the sequence end re-read row S-1: their scores are masked,
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
         if (rmax >= kBc - 1) {
 #pragma unroll
             for (int s = 0; s < T::KSL; ++s)
-                if (w + kWaves * s < T::KCOP) dma16_buf(src, (unsigned)koff[s], Ks + 256 * (w + kWaves * s));
+                if (w + kWaves * s < T::KCOP) dma16_buf(src, koff[s], Ks + 256 * (w + kWaves * s));
         } else {
             int ln = lane;
             asm volatile("" : "+v"(ln));
@@ -165,10 +166,10 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
 #pragma unroll
             for (int s = 0; s < T::VSL; ++s) {
                 if constexpr (kVoffRegs)
-                    dma16_buf(dma_rsrc(vbase + (int64_t)n0 * in_ss), (unsigned)voff[s],
+                    dma16_buf(dma_rsrc(vbase + (int64_t)n0 * in_ss), voff[s],
                               Vs + 256 * (w + kWaves * s));
                 else
-                    dma16_buf(dma_rsrc(vbase + (int64_t)(n0 + T::VROWS * s) * in_ss), (unsigned)voff[0],
+                    dma16_buf(dma_rsrc(vbase + (int64_t)(n0 + T::VROWS * s) * in_ss), voff[0],
                               Vs + 256 * (w + kWaves * s));
             }
         } else {

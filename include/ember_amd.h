@@ -61,6 +61,16 @@ void sync_device(void);
 void ember_empty_cache(void);
 void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak);
 
+/* ---- random tensors: replaces src/random/distributions.h:8-9 ----
+ * (distributions_gpu.cu:11-32; called by src/random/random_api.c:70,88.)
+ * uniform fills out[0..size) with low + (rand()/RAND_MAX)*(high - low) in
+ * fp32, drawn on the host from the C library's rand() -- the generator the
+ * reference binding's _seed() seeds with srand() -- and copied to the
+ * device.  constant sets out[0..size) to value (a fill kernel on the null
+ * stream).  size <= 0 does nothing; errors are recorded as above. */
+void uniform(float low, float high, float *out, int size);
+void constant(float value, float *out, int size);
+
 /* ---- element-wise operators: replaces src/tensor/operators.h:10-18 ----
  * One declaration per row of ember_amd/csrc/operators.def, which lists the
  * same 37 operators as the reference's src/tensor/operators.def:39-82. */
@@ -135,7 +145,13 @@ int attention_fwd(const float *q, const float *k, const float *v, float *o, floa
  * upstream gradient d_o, writes dq, dk, dv (same layout as q, k, v).  P is
  * recomputed from lse; the S x S matrix is never stored.  Needs
  * 2*B*H*S_pad*4 bytes of device scratch (S_pad = S rounded up to 32; none at
- * S <= 32), which the library keeps cached between calls. */
+ * S <= 32), which the library keeps cached between calls.
+ * Determinism: dk and dv are bitwise reproducible.  For S > 32, dq is
+ * accumulated in HBM with fp32 atomic adds from every key block that sees a
+ * query row, so its last bits vary from run to run (each run within the
+ * stated tolerance); at S <= 32 it is reproducible too.  Because of those
+ * atomics dq must be device memory (not host or managed memory), and dq must
+ * not overlap q, k, v, o, lse, d_o, dk or dv. */
 int attention_bwd(const float *q, const float *k, const float *v, const float *o,
                   const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                   int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,

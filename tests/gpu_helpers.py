@@ -10,6 +10,7 @@ import numpy as np
 
 from ember_amd import capi
 from ember_amd.capi import DeviceArray
+from tolerance import gemm_error_bound  # noqa: F401  (re-exported for the GPU tests)
 
 
 def say(msg: str) -> None:
@@ -91,13 +92,3 @@ def gemm_ex(a, b, ta=False, tb=False, bias=None, residual=None, act=0):
                             None if pre is None else pre.ptr, act)
     capi.check(rc, "gemm_ex")
     return (out.numpy(), pre.numpy()) if act else out.numpy()
-
-
-def gemm_error_bound(a, b):
-    """Rigorous bound on |fl(a@b) - a@b| for any fp32 summation order of
-    length k: gamma_k * (|a| @ |b|), gamma_k = k u / (1 - k u), u = 2^-24,
-    doubled for the final rounding and margin."""
-    k = a.shape[-1]
-    u = 2.0 ** -24
-    gamma = k * u / (1 - k * u)
-    return 2.0 * gamma * (np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))) + 1e-30

@@ -240,6 +240,60 @@ def test_packed_qkv_layout(S, D):
     np.testing.assert_allclose(g[:, :, 0].transpose(0, 2, 1, 3), dq_ref, rtol=1e-5, atol=1e-6)
 
 
+def test_row_stride_at_the_guard_edge():
+    """Row stride 2^24 - 4 floats, the largest the entry points accept (rows
+    64 MiB apart): the forward's HBM->LDS copies address a 64-key tile's
+    rows with 32-bit byte offsets up to 4 * 63 * (2^24 - 4), past 2^31.
+    65 heads of S = 96 make the forward take its one-head-per-workgroup
+    kernel; q / k / v of a head sit side by side in each row.  A stride of
+    2^24 is rejected with EMBER_ERR_INVALID_ARGUMENT before any launch."""
+    from ember_amd import capi
+    from ember_amd.capi import DeviceArray
+
+    B, H, S, D = 1, 65, 96, 64
+    ss = (1 << 24) - 4
+    width = 3 * H * D
+    rows = _rand((S, H, 3, D), 950)
+    d_o = _rand((B, H, S, D), 951)
+    q, k, v = (np.ascontiguousarray(rows[:, :, i].transpose(1, 0, 2))[None] for i in range(3))
+    scale = G.scale_for(D)
+    L = capi.lib()
+    G.say(f"row stride {ss} floats: B={B} H={H} S={S} D={D} causal (two {S * ss * 4 / 2**30:.1f} GiB buffers)")
+    buf, gbuf = DeviceArray((S * ss,)), DeviceArray((S * ss,))
+    for r in range(S):
+        L.copy_to_device(buf.ptr + 4 * r * ss, np.ascontiguousarray(rows[r]).ctypes.data, 4 * width)
+    capi.check(what="copy_to_device")
+    o, lse = DeviceArray((B, H, S, D)), DeviceArray((B, H, S))
+    ddo = DeviceArray.from_numpy(d_o)
+    in_st, out_st = (S * ss, 3 * D, ss), capi.contiguous_strides(B, H, S, D)
+    base, gb = buf.ptr, gbuf.ptr
+    capi.check(L.attention_fwd(base, base + 4 * D, base + 8 * D, o.ptr, lse.ptr, B, H, S, D, scale, 1,
+                               *in_st, *out_st), "attention_fwd")
+    capi.check(L.attention_bwd(base, base + 4 * D, base + 8 * D, o.ptr, lse.ptr, ddo.ptr,
+                               gb, gb + 4 * D, gb + 8 * D, B, H, S, D, scale, 1, *in_st, *out_st),
+               "attention_bwd")
+    o_np, lse_np = o.numpy(), lse.numpy()
+    g = np.empty((S, width), np.float32)
+    for r in range(S):
+        L.copy_from_device(g[r].ctypes.data, gb + 4 * r * ss, 4 * width)
+    capi.check(what="copy_from_device")
+    g = g.reshape(S, H, 3, D)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, True, scale)
+    np.testing.assert_allclose(o_np, o_ref, **TOL)
+    np.testing.assert_allclose(lse_np, lse_ref, **TOL)
+    refs = oracle.attention_bwd(q, k, v, o_ref, lse_ref, d_o, True, scale)
+    for i, (name, ref) in enumerate(zip(("dq", "dk", "dv"), refs)):
+        np.testing.assert_allclose(g[:, :, i].transpose(1, 0, 2)[None], ref, err_msg=name, **TOL)
+    del buf, gbuf
+
+    too_far = (S * (1 << 24), 3 * D, 1 << 24)
+    st = L.attention_fwd(o.ptr, o.ptr, o.ptr, o.ptr, lse.ptr, B, H, S, D, scale, 1, *too_far, *out_st)
+    assert st == 1 and L.ember_get_last_error() == 1   # EMBER_ERR_INVALID_ARGUMENT
+    st = L.attention_bwd(o.ptr, o.ptr, o.ptr, o.ptr, lse.ptr, ddo.ptr, o.ptr, o.ptr, o.ptr, B, H, S, D,
+                         scale, 1, *too_far, *out_st)
+    assert st == 1 and L.ember_get_last_error() == 1
+
+
 # ------------------------------------------------------------ long sequences
 
 

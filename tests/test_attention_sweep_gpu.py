@@ -3,9 +3,14 @@
 Each case draws B, H, S, D, the mask and a layout: rows padded past D and
 heads padded past S (strides that are not those of a contiguous tensor),
 separately for the q/k/v/dq/dk/dv and the o/dO triples, so the kernels'
-stride arithmetic, tile tails and launch choices (split-key, packed, wave
-and workgroup forwards) meet shapes no hand-written case lists.  Tolerance
-as everywhere: max-abs 2e-4 / rel 1e-3; padding must stay untouched.
+stride arithmetic and tile tails meet shapes no hand-written case lists.
+The first sweep keeps B, H <= 3, so its launches with S > 64 are small
+(ceil(S/128) * B * H <= 64 workgroups) and take the split-key forward; at
+S <= 64 they take the packed and wave forwards and the short backwards.  The
+second sweep draws enough heads that ceil(S/128) * B * H > 64, which sends
+the forward to the one-head-per-workgroup kernel (attn_fwd_kernel) on the
+same kind of padded strides.  Tolerance as everywhere: max-abs 2e-4 /
+rel 1e-3; padding must stay untouched.
 """
 
 import numpy as np
@@ -33,6 +38,21 @@ def _case(seed):
     return B, H, S, D, causal, pads, hpads
 
 
+def _wide_case(seed):
+    """S > 64 with more than 64 regular (128-query) workgroups."""
+    rng = np.random.default_rng(30_000 + seed)
+    B = int(rng.integers(1, 4))
+    S = int(rng.choice([65, 100, 129, 200, 255, 300, 513, 700]))
+    nqb = -(-S // 128)
+    H = -(-65 // (nqb * B)) + int(rng.integers(0, 6))
+    D = int(rng.choice([32, 64, 128]))
+    causal = bool(rng.integers(0, 2))
+    pads = [int(rng.choice([0, 4, 12, 32])) for _ in range(2)]
+    hpads = [int(rng.choice([0, 1, 3])) for _ in range(2)]
+    assert nqb * B * H > 64
+    return B, H, S, D, causal, pads, hpads
+
+
 def _strided(B, H, S, D, pad, hpad):
     """Strides (sb, sh, ss) of a (B, H, S + hpad, D + pad) buffer."""
     ss = D + pad
@@ -57,7 +77,15 @@ def _download(dev, strides, shape):
 
 @pytest.mark.parametrize("seed", range(64))
 def test_random_shape_and_layout(seed):
-    B, H, S, D, causal, pads, hpads = _case(seed)
+    _run(seed, *_case(seed))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_wide_launch_and_layout(seed):
+    _run(100 + seed, *_wide_case(seed))
+
+
+def _run(seed, B, H, S, D, causal, pads, hpads):
     G.say(f"sweep seed={seed} B={B} H={H} S={S} D={D} causal={causal} pads={pads} hpads={hpads}")
     rng = np.random.default_rng(seed)
     q, k, v, d_o = (rng.standard_normal((B, H, S, D)).astype(np.float32) for _ in range(4))

@@ -1,12 +1,20 @@
 """The C-ABI library loads and exports every symbol include/ember_amd.h
-declares; argument validation rejects bad calls before any device work.
+declares; argument validation rejects bad calls before any device work; and,
+where the reference checkout exists, the reference's own CPython bindings
+link against the library with nothing left undefined.
 CPU only: no call here reaches the HIP runtime."""
 
 import ctypes as C
+import os
+import re
+import subprocess
 
 import pytest
 
 from ember_amd import capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REF = "/root/reference"
 
 # The reference's backend ABI (src/core/memory.h:10-14, src/tensor/operators.h:10-27).
 REFERENCE_SYMBOLS = {
@@ -20,6 +28,7 @@ REFERENCE_SYMBOLS = {
     "add_broadcasted", "sub_broadcasted", "mul_broadcasted", "truediv_broadcasted",
     "negate_tensor", "exponent_tensor", "log_tensor", "sqrt_tensor", "sin_tensor", "cos_tensor",
     "tan_tensor", "ctg_tensor", "sinh_tensor", "cosh_tensor", "tanh_tensor", "ctgh_tensor",
+    "uniform", "constant",   # src/random/distributions.h:8-9
 }
 
 
@@ -73,3 +82,46 @@ def test_capi_raises_on_sticky_error():
     _fwd_call(D=48)
     with pytest.raises(capi.EmberError):
         capi.check()
+
+
+def _nm(path, *flags):
+    out = subprocess.run(["nm", *flags, path], check=True, capture_output=True, text=True).stdout
+    return {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+
+
+def _reference_backend_abi():
+    """Function names the reference's backend headers declare
+    (src/core/memory.h, src/tensor/operators.h with operators.def expanded,
+    src/random/distributions.h), read through the C preprocessor."""
+    src = '#include "memory.h"\n#include "operators.h"\n#include "distributions.h"\n'
+    pre = subprocess.run(["gcc", "-E", "-P", "-x", "c", "-", "-I", f"{REF}/src/core", "-I", f"{REF}/src/tensor",
+                          "-I", f"{REF}/src/random"], input=src, check=True, capture_output=True,
+                         text=True).stdout
+    return set(re.findall(r"\b(\w+)\s*\([^()]*\)\s*;", pre))
+
+
+@pytest.mark.skipif(not os.path.isdir(os.path.join(REF, "src", "random")),
+                    reason="needs the reference checkout (its bindings are compiled, never copied)")
+def test_reference_bindings_link_against_the_library():
+    """The drop-in claim, checked by the linker: the reference's
+    src/tensor/tensor_api.c and src/random/random_api.c, compiled where they
+    lie (oracle/Makefile, target link-check), link as extension modules
+    against libember_amd.so with -Wl,--no-undefined and no backend source of
+    the reference; every backend function they call is exported here, and so
+    is every function the backend headers declare."""
+    subprocess.run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle"), "link-check", f"REF={REF}"],
+                   check=True)
+    link = os.path.join(ROOT, "oracle", "_ref", "link")
+    exports = _nm(capi.LIB_PATH, "-D", "--defined-only")
+    abi = _reference_backend_abi()
+    assert REFERENCE_SYMBOLS == abi
+    assert abi <= exports, sorted(abi - exports)
+    for obj, must in (("tensor_api.o", {"matmul", "matmul_batched", "sum_axis", "alloc_memory"}),
+                      ("random_api.o", {"uniform", "constant", "alloc_memory"})):
+        used = _nm(os.path.join(link, obj), "-u") & abi
+        assert must <= used, obj
+        assert used <= exports, (obj, sorted(used - exports))
+    for mod in ("_tensor.so", "_em_random.so"):
+        dyn = subprocess.run(["readelf", "-d", os.path.join(link, mod)], check=True, capture_output=True,
+                             text=True).stdout
+        assert "[libember_amd.so]" in dyn, mod

@@ -151,3 +151,24 @@ def test_attention_argument_errors():
         em.attention(q, q, np.zeros((2, 4, 16, 64)))
     with pytest.raises(RuntimeError):
         em.nn.Attention(causal=True).backward(q)
+
+
+@pytest.mark.parametrize("module", ["_tensor", "_em_random"])
+def test_type_stubs_match_the_binding_modules(module):
+    """ember_amd/_core/<module>.pyi declares exactly the functions the
+    compiled module exports, with as many parameters as each parses."""
+    import ast
+    import importlib
+    import inspect
+    import os
+
+    mod = importlib.import_module(f"ember_amd._core.{module}")
+    path = os.path.join(os.path.dirname(mod.__file__), f"{module}.pyi")
+    tree = ast.parse(open(path).read())
+    stubbed = {n.name for n in tree.body if isinstance(n, ast.FunctionDef)}
+    exported = {n for n, f in vars(mod).items() if inspect.isbuiltin(f)}
+    assert stubbed == exported, (sorted(stubbed - exported), sorted(exported - stubbed))
+    if module == "_tensor":
+        cls = next(n for n in tree.body if isinstance(n, ast.ClassDef) and n.name == "_Tensor")
+        members = {n.name for n in cls.body if isinstance(n, ast.FunctionDef)} - {"__init__"}
+        assert members <= set(dir(mod._Tensor)), sorted(members - set(dir(mod._Tensor)))

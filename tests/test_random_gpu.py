@@ -66,3 +66,47 @@ def test_seeded_block_is_bitwise_reproducible_over_stale_memory():
     # dQ is accumulated with atomics (order not fixed): gradients agree to
     # rounding, not bitwise.
     np.testing.assert_allclose(g1, g2, rtol=1e-4, atol=1e-5)
+
+
+# ---- the C-ABI entry points the reference's random binding links against
+# (uniform / constant, src/random/distributions.h:8-9)
+
+
+@pytest.mark.parametrize("size", [1, 7, 4096, 100_003])
+def test_capi_uniform_draws_the_c_library_sequence(size):
+    """uniform() draws from the C library's rand() (what the reference
+    binding's _seed() seeds with srand), low + (r / RAND_MAX) * (high - low)
+    in fp32, distributions_gpu.cu:11-24."""
+    from ember_amd import capi
+    from ember_amd.capi import DeviceArray
+
+    G.say(f"capi uniform size={size}")
+    L = capi.lib()
+    libc = ctypes.CDLL("libc.so.6")
+    out = DeviceArray((size,))
+    L.uniform.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_void_p, ctypes.c_int]
+    libc.srand(11)
+    L.uniform(-0.5, 2.0, out.ptr, size)
+    capi.check(what="uniform")
+    (want,) = _libc_uniform(11, [(1, size)], -0.5, 2.0)
+    np.testing.assert_array_equal(out.numpy(), want)
+
+
+@pytest.mark.parametrize("size,offset", [(1, 0), (5, 1), (4096, 0), (4099, 3), (1_000_001, 2)])
+def test_capi_constant_fills_exactly_the_range(size, offset):
+    """constant() sets out[0..size) and nothing else, at any alignment."""
+    from ember_amd import capi
+    from ember_amd.capi import DeviceArray
+
+    G.say(f"capi constant size={size} offset={offset}")
+    L = capi.lib()
+    L.constant.argtypes = [ctypes.c_float, ctypes.c_void_p, ctypes.c_int]
+    buf = DeviceArray.from_numpy(np.full(size + offset + 5, -7.0, np.float32))
+    L.constant(np.float32(0.1), buf.ptr + 4 * offset, size)
+    capi.check(what="constant")
+    got = buf.numpy()
+    assert (got[:offset] == -7.0).all() and (got[offset + size:] == -7.0).all()
+    assert (got[offset:offset + size] == np.float32(0.1)).all()
+    L.constant(np.float32(3.0), buf.ptr, 0)          # size 0: nothing written
+    capi.check(what="constant")
+    assert buf.numpy()[0] == got[0]
