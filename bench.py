@@ -182,15 +182,16 @@ def host_info(threads):
         allowed = len(os.sched_getaffinity(0))
     except (AttributeError, OSError):
         allowed = None
-    return {
-        "cpu_model": model,
-        "host_cores": os.cpu_count(),
-        "affinity_cores": allowed,
-        "threads": threads,
-        "thread_cap": "threads = min(16, os.cpu_count()): a GPU box allots 16 host CPUs to its one GPU's "
-                      "jobs, so an all-cores pool of os.cpu_count() workers is not run; the reference's "
-                      "CPU ops are single-threaded C, one head (or row block) per thread",
-    }
+    cores = os.cpu_count()
+    if cores is not None and threads >= min(cores, allowed or cores):
+        cap = (f"all {min(cores, allowed or cores)} host CPUs this process may use, one worker thread each; "
+               "the reference's CPU ops are single-threaded C, one head (or row block) per thread")
+    else:
+        cap = (f"{threads} of {cores} host CPUs: threads = min(16, os.cpu_count()), because a GPU box allots "
+               "16 host CPUs to its one GPU's jobs; the reference's CPU ops are single-threaded C, one head "
+               "(or row block) per thread")
+    return {"cpu_model": model, "host_cores": cores, "affinity_cores": allowed, "threads": threads,
+            "thread_cap": cap}
 
 
 def cpu_baseline(S, D, threads, inputs, outputs):
