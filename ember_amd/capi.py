@@ -75,6 +75,8 @@ def lib() -> C.CDLL:
     L.attention_fwd.argtypes = [_vp] * 5 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
     L.attention_bwd.restype = C.c_int
     L.attention_bwd.argtypes = [_vp] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
+    L.attention_bwd_noalloc.restype = C.c_int
+    L.attention_bwd_noalloc.argtypes = [_vp] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
     L.softmax_axis.restype = C.c_int
     L.softmax_axis.argtypes = [_vp, _vp, C.c_int, C.c_int, C.c_int]
     L.gemm_ex.restype = C.c_int

@@ -14,6 +14,8 @@
 // D = 128, while for non-causal D = 128 the default allocation cycles the
 // 128 dK/dV accumulators between AGPRs and VGPRs every query block and runs
 // 2x slower than the VGPR form (and D = 64 causal is 6 % faster in VGPR form).
+#include <mutex>
+
 #include "attention_bwd_kernels.h"
 
 namespace ember {
@@ -356,16 +358,63 @@ int launch_bwd_short(const BwdArgs &args, int nbh)
 }  // namespace
 }  // namespace ember
 
-extern "C" int attention_bwd(const float *q, const float *k, const float *v, const float *o,
-                             const float *lse, const float *d_o, float *dq, float *dk, float *dv,
-                             int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
-                             int64_t in_sb, int64_t in_sh, int64_t in_ss, int64_t out_sb,
-                             int64_t out_sh, int64_t out_ss)
+// Row statistics of the no-allocation entry point: a fixed device array,
+// one per GPU (each device that loads this library holds its own copy until
+// the process ends).  2^22 floats = 16 MiB, i.e. lse2 and delta for up to
+// 2^21 padded rows (B * H * S_pad).  Host code never uses this name as an
+// address: the device address comes from hipGetSymbolAddress, once per
+// device (noalloc_stats below).
+static __device__ __align__(256) float scratch[size_t(1) << 22];
+
+namespace ember {
+namespace {
+
+constexpr size_t kNoAllocStatsFloats = size_t(1) << 22;
+constexpr int kNoAllocDevices = 16;
+
+// Where attention_bwd_rows puts the row statistics (2 * rows_pad floats):
+// sets *out and returns EMBER_OK, or returns the status it recorded.
+using StatsSource = int (*)(int64_t rows_pad, float **out);
+
+int library_stats(int64_t rows_pad, float **out)
 {
-    using namespace ember;
+    *out = (float *)scratch(kScratchAttnDelta, (size_t)rows_pad * 2 * sizeof(float));
+    return *out ? EMBER_OK : EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
+}
+
+std::mutex g_noalloc_mu;
+float *g_noalloc_ptr[kNoAllocDevices];
+
+int noalloc_stats(int64_t rows_pad, float **out)
+{
+    if ((size_t)rows_pad * 2 > kNoAllocStatsFloats)
+        return record_error(EMBER_ERR_INVALID_ARGUMENT,
+                            "attention_bwd_noalloc: B*H*S_pad (S rounded up to 32) exceeds 2^21 rows");
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return EMBER_ERR_DEVICE;
+    if (dev < 0 || dev >= kNoAllocDevices)
+        return record_error(EMBER_ERR_UNSUPPORTED, "attention_bwd_noalloc: device index");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        float *ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(::scratch));
+        if (err != hipSuccess || !ptr)
+            return record_error(EMBER_ERR_DEVICE, "hipGetSymbolAddress(attention_bwd_noalloc scratch)", err);
+        g_noalloc_ptr[dev] = ptr;
+    }
+    *out = g_noalloc_ptr[dev];
+    return EMBER_OK;
+}
+
+int attention_bwd_rows(const float *q, const float *k, const float *v, const float *o,
+                       const float *lse, const float *d_o, float *dq, float *dk, float *dv, int64_t B,
+                       int64_t H, int64_t S, int64_t D, float scale, int causal, int64_t in_sb,
+                       int64_t in_sh, int64_t in_ss, int64_t out_sb, int64_t out_sh, int64_t out_ss,
+                       StatsSource stats_source, const char *who)
+{
     const void *ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv};
     const int64_t strides[] = {in_sb, in_sh, in_ss, out_sb, out_sh, out_ss};
-    int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, "attention_bwd");
+    int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, who);
     if (st != EMBER_OK || B * H * S == 0) return st;
 
     // S <= 32: one or two waves per head (attn_bwd_short; measured 1.5-3x
@@ -405,8 +454,9 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
-    float *stats = (float *)scratch(kScratchAttnDelta, (size_t)rows_pad * 2 * sizeof(float));
-    if (!stats) return EMBER_ERR_OUT_OF_MEMORY;
+    float *stats = nullptr;
+    st = stats_source(rows_pad, &stats);
+    if (st != EMBER_OK) return st;
 
     BwdArgs args;
     args.q = q;
@@ -452,4 +502,37 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
         case 256: return launch_bwd<128, false>(args, rows_pad, nblocks);
         default: return launch_bwd_causal_d128(args, rows_pad, nblocks);
     }
+}
+
+}  // namespace
+}  // namespace ember
+
+extern "C" int attention_bwd(const float *q, const float *k, const float *v, const float *o,
+                             const float *lse, const float *d_o, float *dq, float *dk, float *dv,
+                             int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
+                             int64_t in_sb, int64_t in_sh, int64_t in_ss, int64_t out_sb,
+                             int64_t out_sh, int64_t out_ss)
+{
+    return ember::attention_bwd_rows(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale, causal, in_sb,
+                                     in_sh, in_ss, out_sb, out_sh, out_ss, ember::library_stats,
+                                     "attention_bwd");
+}
+
+// The same computation with the row statistics in the fixed array above:
+// no hipMalloc, hipFree or other allocating call on any path (the first call
+// on a device looks up the array's device address).  Every thread and call
+// on one device shares that device's array; the library enqueues all work on
+// the null stream, so calls run one after another, and launches of this entry
+// point that overlap on one device would race on the array.  Each call writes
+// every statistic it reads (attn_bwd_pre fills all 2 * rows_pad floats,
+// padding rows included) before reading it, so nothing needs clearing.
+extern "C" int attention_bwd_noalloc(const float *q, const float *k, const float *v, const float *o,
+                                     const float *lse, const float *d_o, float *dq, float *dk,
+                                     float *dv, int64_t B, int64_t H, int64_t S, int64_t D,
+                                     float scale, int causal, int64_t in_sb, int64_t in_sh,
+                                     int64_t in_ss, int64_t out_sb, int64_t out_sh, int64_t out_ss)
+{
+    return ember::attention_bwd_rows(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale, causal, in_sb,
+                                     in_sh, in_ss, out_sb, out_sh, out_ss, ember::noalloc_stats,
+                                     "attention_bwd_noalloc");
 }

@@ -158,6 +158,25 @@ int attention_bwd(const float *q, const float *k, const float *v, const float *o
                   int64_t in_sb, int64_t in_sh, int64_t in_ss,
                   int64_t out_sb, int64_t out_sh, int64_t out_ss);
 
+/* attention_bwd without any device allocation.  No counterpart in the
+ * reference.  It is for callers that cannot allocate device memory during the
+ * call: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Same arguments, kernels, results and errors as
+ * attention_bwd, except where the row statistics live: a fixed 16 MiB device
+ * array inside the library, one per GPU, held until the process ends, instead
+ * of library-allocated scratch.  Limit: B*H*S_pad <= 2^21 rows (S_pad = S
+ * rounded up to 32); a larger call returns EMBER_ERR_INVALID_ARGUMENT and
+ * launches nothing.  Every call on one GPU shares that GPU's array.  Calls
+ * are ordered because all library work runs on the null stream; launches of
+ * this entry point that overlap on one GPU (for example replayed on several
+ * streams at once) race on the array.  Each call writes every statistic it
+ * reads before reading it, so nothing carries over between calls. */
+int attention_bwd_noalloc(const float *q, const float *k, const float *v, const float *o,
+                          const float *lse, const float *d_o, float *dq, float *dk, float *dv,
+                          int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
+                          int64_t in_sb, int64_t in_sh, int64_t in_ss,
+                          int64_t out_sb, int64_t out_sh, int64_t out_ss);
+
 /* ---- fused Adam: replaces ember/optim/adam.py:24-45 (Adam.apply) ----
  *
  * One Adam step over `ntensors` parameter tensors in as few launches as
