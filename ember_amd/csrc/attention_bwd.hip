@@ -1,7 +1,8 @@
 // attention_bwd.hip -- entry point of the fused flash-attention backward
 // (fp32, gfx950); the workgroup kernels are in attention_bwd_kernels.h, the
-// short-sequence kernels (S <= 32: one or two waves per head; 32 < S <= 64
-// at D <= 64: one wave per key block) are below.
+// short-sequence kernels (S <= 32: one wave per head at D <= 64, one
+// workgroup per head with LDS-staged tiles at D = 128; 32 < S <= 64 at
+// D <= 64: one wave per key block) are below.
 //
 // No reference counterpart (pawel002/ember has no attention): the operator is
 // new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
@@ -21,10 +22,10 @@
 namespace ember {
 namespace {
 
-// Short sequences (S <= 32): WPH waves per (b, h) (1, or 2 at D = 128) do
-// the whole head, a single 32 x 32 block; four independent waves per
-// workgroup, no workgroup barriers, no atomics and no scratch (the row
-// statistics are formed in the kernel).
+// Short sequences (S <= 32) at D <= 64: one wave per (b, h) does the whole
+// head, a single 32 x 32 block; four independent waves per workgroup, no
+// workgroup barriers, no atomics and no scratch (the row statistics are
+// formed in the kernel).
 //   S = Q K^T, dP = dO V^T                       (C[m][n]: keys on lanes)
 //   P = exp2(S*c - lse2), dS = P * (dP - delta)
 // then, 32 columns of d at a time,
@@ -33,14 +34,11 @@ namespace {
 //                                                 wave's own LDS tile)
 // Q, K, dO, V rows are read one row per lane (row = lane % 32, half of D
 // per lane half) for the S / dP products and as 32-float row segments for
-// the others; rows past S are read as row S-1 and carry P = 0.  With two
-// waves per head both form S, dP, P and dS and each writes half of the
-// columns of dV, dK and dQ, which halves the per-wave chain of dependent
-// loads (one wave per head at D = 128 was slower than the workgroup kernel).
-template <int D, bool CAUSAL, int WPH>
+// the others; rows past S are read as row S-1 and carry P = 0.
+template <int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh)
 {
-    static_assert(WPH == 1 || (WPH == 2 && D >= 64), "waves per head");
+    static_assert(D <= 64, "D = 128 takes attn_bwd_short_lds");
     constexpr int DH = D / 2;
     constexpr int DB = D / 32;
     constexpr int TSTR = 36;  // padded row of the 32 x 32 dS tile
@@ -51,10 +49,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
-    const int bh = (blockIdx.x * kWaves + w) / WPH;
+    const int bh = blockIdx.x * kWaves + w;
     if (bh >= nbh) return;  // no barriers below
-    const int db0 = WPH == 1 ? 0 : (w & 1) * (DB / 2);
-    constexpr int NDB = DB / WPH;
+    constexpr int db0 = 0;
+    constexpr int NDB = DB;
     const int b = bh / a.H;
     const int hh = bh - b * a.H;
     const int S = a.S;
@@ -331,6 +329,177 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short2(BwdArgs a, int nb
     }
 }
 
+// Short sequences at D = 128 (S <= 32): one workgroup of 4 waves per head,
+// the head's Q, K, V and dO staged in LDS by direct HBM -> LDS copies
+// (coalesced 1 KiB copies, no registers), so every operand the products
+// read row-by-lane comes from LDS instead of from scattered 16-byte global
+// loads.  Per head:
+//   copies of Q, K, V, dO (padded rows of D+4 floats); meanwhile each wave
+//   forms delta = <dO, O> for 8 rows from coalesced global reads of O and dO
+//   (8 lanes per row) and lse2 = lse * log2(e);
+//   wave w: S and dP of the 16 x 16 quadrant (queries 16(w/2).., keys
+//   16(w%2)..) on v_mfma_f32_16x16x4f32 over all of D (a causal head skips
+//   the quadrant above the diagonal), then P and dS of the quadrant, stored
+//   transposed ([key][query]) in LDS;
+//   wave w: columns 32w..32w+31 of dV = P^T dO, dK = scale dS^T Q and
+//   dQ = scale dS K on v_mfma_f32_32x32x2f32 (contraction over the 32
+//   queries or keys in the order q = (s & 7) + 8h + 16(s >> 3) for k-step s
+//   and lane half h, which puts the two lane halves' LDS rows 8 apart, in
+//   disjoint banks).
+// Rows past S are copied as row S-1 and carry lse2 = +inf (P = 0), delta = 0.
+// Two workgroups per CU (79 KB of LDS each).
+struct ShortLds {
+    static constexpr int D = 128;
+    static constexpr int STR = D + 4;                 // padded tile row (floats)
+    static constexpr int ROWCH = STR / 4;             // 16-byte chunks per padded row
+    static constexpr int COP = (kBq * ROWCH + 63) / 64;  // 1 KiB copies per tile
+    static constexpr int TILE = COP * 256;            // floats reserved per tile
+    static constexpr int PSTR = kBq + 4;              // padded row of P^T / dS^T
+};
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_short_lds(BwdArgs a)
+{
+    typedef ShortLds L;
+    constexpr int D = L::D;
+    __shared__ float tiles[4 * L::TILE];  // Q, K, V, dO
+    __shared__ float PT[kBq * L::PSTR], DT[kBq * L::PSTR];
+    __shared__ float L2s[kBq], DLs[kBq];
+    float *__restrict__ Qs = tiles;
+    float *__restrict__ Ks = tiles + L::TILE;
+    float *__restrict__ Vs = tiles + 2 * L::TILE;
+    float *__restrict__ Gs = tiles + 3 * L::TILE;
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int bh = blockIdx.x;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
+
+    // ---- copies: copy t of a tile fills chunks 64t..64t+63 (row p / ROWCH,
+    // chunk p % ROWCH); the padding chunk and the slack past the tile re-read
+    // the tile's first chunk ----
+    {
+        const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
+        const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
+        const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
+        const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
+#pragma unroll
+        for (int t = w; t < L::COP; t += kWaves) {
+            const int p = 64 * t + lane;
+            int r = p / L::ROWCH;
+            const int c = p - r * L::ROWCH;
+            const bool real = r < kBq && c < D / 4;
+            r = r < S ? r : S - 1;
+            const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
+            const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
+            dma16_buf(rq, oi, Qs + 256 * t);
+            dma16_buf(rk, oi, Ks + 256 * t);
+            dma16_buf(rv, oi, Vs + 256 * t);
+            dma16_buf(rg, og, Gs + 256 * t);
+        }
+    }
+    // ---- row statistics of rows 8w..8w+7: 8 lanes per row ----
+    {
+        const int j = 8 * w + (lane >> 3);
+        const int s8 = lane & 7;
+        const int jr = j < S ? j : S - 1;
+        const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
+        const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
+        float part = 0.0f;
+#pragma unroll
+        for (int it = 0; it < D / 32; ++it) {
+            const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
+            const f32x4 g4 = *(const f32x4 *)(grow + 32 * it + 4 * s8);
+            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
+        }
+        part += __shfl_xor(part, 1);
+        part += __shfl_xor(part, 2);
+        part += __shfl_xor(part, 4);
+        if (s8 == 0) {
+            L2s[j] = j < S ? a.lse[(int64_t)bh * S + j] * kLog2e : INFINITY;
+            DLs[j] = j < S ? part : 0.0f;
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+
+    // ---- S, dP, P, dS of quadrant (qm, qn) ----
+    {
+        const int qm = w >> 1, qn = w & 1;
+        const int l16 = lane & 15, g4 = lane >> 4;
+        const int key = 16 * qn + l16;
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+        if (!CAUSAL || qn <= qm) {
+            const int arow = (16 * qm + l16) * L::STR + 4 * g4;
+            const int brow = key * L::STR + 4 * g4;
+#pragma unroll
+            for (int c0 = 0; c0 < D; c0 += 16) {
+                const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
+                const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
+                const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
+                const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[j], kf[j], sacc, 0, 0, 0);
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[j], vf[j], pacc, 0, 0, 0);
+                }
+            }
+        }
+        // C[m][n] of the quadrant: lane (n = l16, g4), register r: m = 4 g4 + r.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int qi = 16 * qm + 4 * g4 + r;
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
+            const bool vis = key < S && (!CAUSAL || key <= qi);
+            p = vis ? p : 0.0f;
+            PT[key * L::PSTR + qi] = p;
+            DT[key * L::PSTR + qi] = p * (pacc[r] - DLs[qi]);
+        }
+    }
+    __syncthreads();
+
+    // ---- columns 32w.. of dV, dK, dQ ----
+    const int h32 = lane >> 5, l32 = lane & 31;
+    const int col = 32 * w + l32;
+    f32x16 dv = zero16(), dk = zero16(), dq = zero16();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        // k-steps s = 4t..4t+3 contract rows q = (s & 7) + 8 h32 + 16 (s >> 3)
+        const int q0 = 4 * (t & 1) + 8 * h32 + 16 * (t >> 1);
+        const f32x4 pt = *(const f32x4 *)&PT[l32 * L::PSTR + q0];
+        const f32x4 dt = *(const f32x4 *)&DT[l32 * L::PSTR + q0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int q = q0 + j;
+            dv = mfma_32x32x2(pt[j], Gs[q * L::STR + col], dv);
+            dk = mfma_32x32x2(dt[j], Qs[q * L::STR + col], dk);
+            dq = mfma_32x32x2(DT[q * L::PSTR + l32], Ks[q * L::STR + col], dq);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = acc_row(i, h32);
+        if (r < S) {
+            const int64_t off = in_base + (int64_t)r * in_ss + col;
+            a.dv[off] = dv[i];
+            a.dk[off] = dk[i] * a.scale;
+            a.dq[off] = dq[i] * a.scale;
+        }
+    }
+}
+
+template <bool CAUSAL>
+int launch_bwd_short_lds(const BwdArgs &args, int nbh)
+{
+    hipLaunchKernelGGL((attn_bwd_short_lds<CAUSAL>), dim3((unsigned)nbh), dim3(kThreads), 0, 0, args);
+    return launch_ok("attn_bwd_short_lds") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
 template <int D, bool CAUSAL>
 int launch_bwd_short2(const BwdArgs &args, int64_t rows_pad, int nbh)
 {
@@ -346,12 +515,8 @@ int launch_bwd_short2(const BwdArgs &args, int64_t rows_pad, int nbh)
 template <int D, bool CAUSAL>
 int launch_bwd_short(const BwdArgs &args, int nbh)
 {
-    // Two waves per head at D = 128 (1.6 -> 2.4 TB/s at S = 32: half the
-    // chain of dependent loads per wave); one at D <= 64 (two measured 2.3
-    // against 3.3 TB/s there).
-    constexpr int WPH = D == 128 ? 2 : 1;
-    const dim3 grid((unsigned)(((int64_t)nbh * WPH + kWaves - 1) / kWaves));
-    hipLaunchKernelGGL((attn_bwd_short<D, CAUSAL, WPH>), grid, dim3(kThreads), 0, 0, args, nbh);
+    const dim3 grid((unsigned)(((int64_t)nbh + kWaves - 1) / kWaves));
+    hipLaunchKernelGGL((attn_bwd_short<D, CAUSAL>), grid, dim3(kThreads), 0, 0, args, nbh);
     return launch_ok("attn_bwd_short") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
@@ -417,8 +582,10 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, who);
     if (st != EMBER_OK || B * H * S == 0) return st;
 
-    // S <= 32: one or two waves per head (attn_bwd_short; measured 1.5-3x
-    // the workgroup kernel's throughput there).
+    // S <= 32: one wave per head at D <= 64 (attn_bwd_short; measured
+    // 1.5-3x the workgroup kernel's throughput there) and one LDS-staged
+    // workgroup per head at D = 128 (attn_bwd_short_lds: 4.8 TB/s at S = 32,
+    // against 2.8 for two register-fed waves per head).
     if (S <= kBq) {
         BwdArgs sa;
         sa.q = q;
@@ -448,8 +615,8 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
             case 65: return launch_bwd_short<32, true>(sa, nbh);
             case 128: return launch_bwd_short<64, false>(sa, nbh);
             case 129: return launch_bwd_short<64, true>(sa, nbh);
-            case 256: return launch_bwd_short<128, false>(sa, nbh);
-            default: return launch_bwd_short<128, true>(sa, nbh);
+            case 256: return launch_bwd_short_lds<false>(sa, nbh);
+            default: return launch_bwd_short_lds<true>(sa, nbh);
         }
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
