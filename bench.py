@@ -250,7 +250,7 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
     """Attention where it is HBM-bound: the forward at S = 32, 64, 128 and
     D = 128, causal, 2^20 query rows per tensor (the shapes `secondary`
     reports), achieved bandwidth over the algorithmic bytes 16*B*H*S*D +
-    4*B*H*S; then the backward at S = 32 (D = 64, 128) and S = 64 (D = 128).  With
+    4*B*H*S; then the backward at S = 32, 64, 128 (D = 64, 128).  With
     copy_probe_mb, one negate_tensor pass over that many MiB follows (known
     bytes for scaling the traffic counters)."""
     out = {}
@@ -272,9 +272,11 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
                                   "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
         del q, k, v, o, lse
     # The backward in the same regime: algorithmic bytes 32*B*H*S*D + 8*B*H*S
-    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 32 takes the
-    # short-sequence kernel (one wave per head, two at D = 128).
-    for S, D in ((32, 64), (32, 128), (64, 128)):
+    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 32: one wave per head
+    # (D = 64) or one LDS-staged workgroup per head (D = 128); S = 64: one wave
+    # per key block (D = 64) or the workgroup kernel (D = 128); S = 128: the
+    # workgroup kernel.
+    for S, D in ((32, 64), (32, 128), (64, 64), (64, 128), (128, 64), (128, 128)):
         B, H = (1 << 20) // S // 64, 64
         n = B * H * S * D
         q, k, v, g = (DeviceArray((n,), rng.standard_normal(n, dtype=np.float32)) for _ in range(4))
@@ -381,9 +383,13 @@ def secondary(L, ev):
     attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20)
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
-    # The backward where it is HBM-bound (S <= 32: one wave per head, two at D = 128).
-    attn("short_s32_d64_fwd_bwd", (1 << 20) // 32 // 64, 64, 32, 64, True, True, 20)
-    attn("short_s32_d128_fwd_bwd", (1 << 20) // 32 // 64, 64, 32, 128, True, True, 20)
+    # The backward where it is HBM-bound (AI = S/8 causal): S = 32 (one wave
+    # per head at D = 64, one LDS-staged workgroup per head at D = 128),
+    # S = 64 (one wave per key block at D = 64, the workgroup kernel at
+    # D = 128) and S = 128 (the workgroup kernel).
+    for S in (32, 64, 128):
+        for D in (64, 128):
+            attn(f"short_s{S}_d{D}_fwd_bwd", (1 << 20) // S // 64, 64, S, D, True, True, 20)
 
     # Fused Adam over config 5's parameters (pre-LN decoder block, d=1024,
     # MLP 4x): LN gains/biases, QKV, out-proj, MLP weights and biases.
@@ -469,6 +475,48 @@ def secondary(L, ev):
     return out, keep
 
 
+def vendor_gemm_ab(reps=6):
+    """This library's matmul against the vendor's fp32 GEMM (torch.matmul on
+    ROCm: hipBLASLt) on the config-4 and config-5 shapes, alternating the two
+    in one process with the same inputs, so both see the same clock and
+    thermal state (the GPU's clock under sustained fp32 MFMA load is power
+    limited, so figures taken at different moments are not comparable).  The
+    vendor library is measured, never used by the product."""
+    import torch
+
+    L = capi.lib()
+    out = {}
+    for n, k, m in ((4096, 4096, 4096), (16384, 1024, 3072), (8192, 1024, 3072), (8192, 4096, 1024)):
+        rng = np.random.default_rng(7)
+        a = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, (k, m)).astype(np.float32)
+        da, db, dc = DeviceArray.from_numpy(a), DeviceArray.from_numpy(b), DeviceArray((n, m))
+        ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+        fns = {"ember_amd": lambda: L.matmul(da.ptr, db.ptr, dc.ptr, n, m, k),
+               "vendor": lambda: torch.matmul(ta, tb)}
+        ms = {name: [] for name in fns}
+        for rep in range(reps):
+            order = list(fns) if rep % 2 == 0 else list(fns)[::-1]
+            for name in order:
+                for _ in range(3):
+                    fns[name]()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(10):
+                    fns[name]()
+                e1.record()
+                torch.cuda.synchronize()
+                ms[name].append(e0.elapsed_time(e1) / 10)
+        capi.check(what="matmul")
+        fl = 2.0 * n * m * k
+        out[f"{n}x{k}x{m}"] = {name: {"median_tflops": round(fl / float(np.median(v)) / 1e9, 1),
+                                      "min_tflops": round(fl / max(v) / 1e9, 1),
+                                      "max_tflops": round(fl / min(v) / 1e9, 1)} for name, v in ms.items()}
+        del da, db, dc, ta, tb
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -494,12 +542,18 @@ def main(argv=None):
     ap.add_argument("--decoder-steps", type=int, default=0,
                     help="only run config 5's decoder-block training step this many "
                          "times and print its record (for profiling)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only compare this library's matmul with the vendor fp32 GEMM "
+                         "(torch.matmul), alternating in one process, and print the record")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on exactly one GPU (no multi-GPU path); "
               "use --gpus 1", file=sys.stderr)
         return 2
+    if args.vendor_gemm:
+        print(json.dumps({"gemm_vs_vendor": vendor_gemm_ab()}), flush=True)
+        return 0
     if args.decoder_steps > 0:
         print(json.dumps({"config5_decoder_step": decoder_step(8, 1024, 1024, 16, args.decoder_steps)}),
               flush=True)

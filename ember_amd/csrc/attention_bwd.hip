@@ -493,6 +493,193 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short_lds(BwdArgs a)
     }
 }
 
+// 32 < S <= 64 at D = 128: the same scheme with 64-row tiles, one
+// workgroup of 8 waves per head (one per CU: Q, K, dO and V take 132 KB).
+// P^T and dS^T (64 x 68 floats each) overlay the V tile once every wave is
+// past its dP products, so P and dS wait in registers across one barrier.
+//   wave w: S / dP quadrants w and w + 8 of the 4 x 4 grid of 16 x 16
+//   quadrants (a causal head skips those above the diagonal);
+//   wave w: rows 32(w/4).. and columns 32(w%4).. of dV, dK and dQ, over the
+//   64 queries / keys (a causal head skips the half that is all zeros: keys
+//   32.. see only queries 32.., queries 0..31 only keys 0..31).
+struct ShortLds64 {
+    static constexpr int D = 128;
+    static constexpr int R = 64;                         // rows per tile
+    static constexpr int NW = 8;                         // waves
+    static constexpr int STR = D + 4;
+    static constexpr int ROWCH = STR / 4;
+    static constexpr int COP = (R * ROWCH + 63) / 64;    // 33 copies per tile
+    static constexpr int TILE = COP * 256;
+    static constexpr int PSTR = R + 4;                   // P^T / dS^T row
+    static constexpr int VP = TILE > 2 * R * PSTR ? TILE : 2 * R * PSTR;
+};
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64(BwdArgs a)
+{
+    typedef ShortLds64 L;
+    constexpr int D = L::D, R = L::R;
+    __shared__ float tiles[3 * L::TILE + L::VP];  // Q, K, dO, then V (later P^T, dS^T)
+    __shared__ float L2s[R], DLs[R];
+    float *__restrict__ Qs = tiles;
+    float *__restrict__ Ks = tiles + L::TILE;
+    float *__restrict__ Gs = tiles + 2 * L::TILE;
+    float *__restrict__ Vs = tiles + 3 * L::TILE;
+    float *__restrict__ PT = Vs;
+    float *__restrict__ DT = Vs + R * L::PSTR;
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int bh = blockIdx.x;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
+
+    {
+        const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
+        const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
+        const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
+        const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
+#pragma unroll
+        for (int t = w; t < L::COP; t += L::NW) {
+            const int p = 64 * t + lane;
+            int r = p / L::ROWCH;
+            const int c = p - r * L::ROWCH;
+            const bool real = r < R && c < D / 4;
+            r = r < S ? r : S - 1;
+            const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
+            const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
+            dma16_buf(rq, oi, Qs + 256 * t);
+            dma16_buf(rk, oi, Ks + 256 * t);
+            dma16_buf(rv, oi, Vs + 256 * t);
+            dma16_buf(rg, og, Gs + 256 * t);
+        }
+    }
+    {
+        const int j = 8 * w + (lane >> 3);
+        const int s8 = lane & 7;
+        const int jr = j < S ? j : S - 1;
+        const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
+        const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
+        float part = 0.0f;
+#pragma unroll
+        for (int it = 0; it < D / 32; ++it) {
+            const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
+            const f32x4 g4 = *(const f32x4 *)(grow + 32 * it + 4 * s8);
+            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
+        }
+        part += __shfl_xor(part, 1);
+        part += __shfl_xor(part, 2);
+        part += __shfl_xor(part, 4);
+        if (s8 == 0) {
+            L2s[j] = j < S ? a.lse[(int64_t)bh * S + j] * kLog2e : INFINITY;
+            DLs[j] = j < S ? part : 0.0f;
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+
+    // ---- S, dP, P, dS of quadrants w and w + 8 ----
+    const int l16 = lane & 15, g4 = lane >> 4;
+    float pv[2][4], dv4[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int quad = w + 8 * u;
+        const int qm = quad >> 2, qn = quad & 3;
+        const int key = 16 * qn + l16;
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+        if (!CAUSAL || qn <= qm) {
+            const int arow = (16 * qm + l16) * L::STR + 4 * g4;
+            const int brow = key * L::STR + 4 * g4;
+#pragma unroll
+            for (int c0 = 0; c0 < D; c0 += 16) {
+                const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
+                const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
+                const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
+                const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[j], kf[j], sacc, 0, 0, 0);
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[j], vf[j], pacc, 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int qi = 16 * qm + 4 * g4 + r;
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
+            const bool vis = key < S && (!CAUSAL || key <= qi);
+            p = vis ? p : 0.0f;
+            pv[u][r] = p;
+            dv4[u][r] = p * (pacc[r] - DLs[qi]);
+        }
+    }
+    __syncthreads();  // every wave is past its dP products: V's space is free
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int quad = w + 8 * u;
+        const int qm = quad >> 2, qn = quad & 3;
+        const int key = 16 * qn + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int qi = 16 * qm + 4 * g4 + r;
+            PT[key * L::PSTR + qi] = pv[u][r];
+            DT[key * L::PSTR + qi] = dv4[u][r];
+        }
+    }
+    __syncthreads();
+
+    // ---- rows 32 rb.., columns 32 cb.. of dV, dK (rows: keys) and dQ (rows: queries) ----
+    const int h32 = lane >> 5, l32 = lane & 31;
+    const int rb = w >> 2;
+    const int col = 32 * (w & 3) + l32;
+    const int row = 32 * rb + l32;
+    f32x16 dv = zero16(), dk = zero16(), dq = zero16();
+    // k-steps s = 4t..4t+3 contract q = (s & 7) + 8 h32 + 16 (s >> 3); causal:
+    // keys 32.. (rb = 1) see queries >= 32 only (t >= 4), queries 0..31
+    // (rb = 0) see keys < 32 only (t < 4).
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int q0 = 4 * (t & 1) + 8 * h32 + 16 * (t >> 1);
+        const bool kv_live = !CAUSAL || rb == 0 || t >= 4;
+        const bool q_live = !CAUSAL || rb == 1 || t < 4;
+        if (kv_live) {
+            const f32x4 pt = *(const f32x4 *)&PT[row * L::PSTR + q0];
+            const f32x4 dt = *(const f32x4 *)&DT[row * L::PSTR + q0];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dv = mfma_32x32x2(pt[j], Gs[(q0 + j) * L::STR + col], dv);
+                dk = mfma_32x32x2(dt[j], Qs[(q0 + j) * L::STR + col], dk);
+            }
+        }
+        if (q_live) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                dq = mfma_32x32x2(DT[(q0 + j) * L::PSTR + row], Ks[(q0 + j) * L::STR + col], dq);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 32 * rb + acc_row(i, h32);
+        if (r < S) {
+            const int64_t off = in_base + (int64_t)r * in_ss + col;
+            a.dv[off] = dv[i];
+            a.dk[off] = dk[i] * a.scale;
+            a.dq[off] = dq[i] * a.scale;
+        }
+    }
+}
+
+template <bool CAUSAL>
+int launch_bwd_short_lds64(const BwdArgs &args, int nbh)
+{
+    hipLaunchKernelGGL((attn_bwd_short_lds64<CAUSAL>), dim3((unsigned)nbh), dim3(512), 0, 0, args);
+    return launch_ok("attn_bwd_short_lds64") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
 template <bool CAUSAL>
 int launch_bwd_short_lds(const BwdArgs &args, int nbh)
 {
@@ -618,6 +805,34 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
             case 256: return launch_bwd_short_lds<false>(sa, nbh);
             default: return launch_bwd_short_lds<true>(sa, nbh);
         }
+    }
+    // 32 < S <= 64 at D = 128: one 8-wave workgroup per head, LDS-staged
+    // (attn_bwd_short_lds64); like the S <= 32 kernels it needs no scratch.
+    if (S <= 2 * kBq && D == 128) {
+        BwdArgs sa;
+        sa.q = q;
+        sa.k = k;
+        sa.v = v;
+        sa.o = o;
+        sa.lse = lse;
+        sa.dout = d_o;
+        sa.dq = dq;
+        sa.dk = dk;
+        sa.dv = dv;
+        sa.lse2 = sa.delta = nullptr;
+        sa.H = (int)H;
+        sa.S = (int)S;
+        sa.S_pad = sa.nkb = 0;
+        sa.c = scale * kLog2e;
+        sa.scale = scale;
+        sa.in_sb = in_sb;
+        sa.in_sh = in_sh;
+        sa.in_ss = in_ss;
+        sa.out_sb = out_sb;
+        sa.out_sh = out_sh;
+        sa.out_ss = out_ss;
+        return causal ? launch_bwd_short_lds64<true>(sa, (int)(B * H))
+                      : launch_bwd_short_lds64<false>(sa, (int)(B * H));
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;

@@ -10,6 +10,7 @@ import gpu_helpers as G
 import oracle
 from ember_amd import Tensor, _core, loss, nn, optim
 from oracle import decoder
+from tolerance import assert_north_star
 
 pytestmark = pytest.mark.gpu
 
@@ -138,11 +139,10 @@ def test_decoder_block_matches_oracle(causal):
     dx = block.backward(Tensor(dy))
     y_ref, cache = decoder.forward(params, x, B, S, H, causal)
     dx_ref, g_ref = decoder.backward(params, cache, dy, B, S, H)
-    tol = dict(rtol=2e-3, atol=2e-4)
-    np.testing.assert_allclose(y.to_np(), y_ref, **tol)
-    np.testing.assert_allclose(dx.to_np(), dx_ref, **tol)
+    assert_north_star(y.to_np(), y_ref, "y")
+    assert_north_star(dx.to_np(), dx_ref, "dx")
     for i, (got, ref) in enumerate(zip(block.gradients(), g_ref)):
-        np.testing.assert_allclose(got.to_np(), ref, err_msg=f"grad {i}", **tol)
+        assert_north_star(got.to_np(), ref, f"grad {i}")
 
 
 def test_decoder_training_step_reduces_the_loss():
