@@ -1,8 +1,7 @@
 // attention_bwd.hip -- entry point of the fused flash-attention backward
-// (fp32, gfx950); the workgroup kernels are in attention_bwd_kernels.h, the
-// short-sequence kernels (S <= 32: one wave per head at D <= 64, one
-// workgroup per head with LDS-staged tiles at D = 128; 32 < S <= 64 at
-// D <= 64: one wave per key block) are below.
+// (fp32, gfx950); the workgroup kernels (S > 64) are in
+// attention_bwd_kernels.h, the short-sequence kernels (S <= 64: one
+// workgroup per head with Q, K, V, dO staged in LDS) are below.
 //
 // No reference counterpart (pawel002/ember has no attention): the operator is
 // new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
@@ -21,313 +20,6 @@
 
 namespace ember {
 namespace {
-
-// Short sequences (S <= 32) at D <= 64: one wave per (b, h) does the whole
-// head, a single 32 x 32 block; four independent waves per workgroup, no
-// workgroup barriers, no atomics and no scratch (the row statistics are
-// formed in the kernel).
-//   S = Q K^T, dP = dO V^T                       (C[m][n]: keys on lanes)
-//   P = exp2(S*c - lse2), dS = P * (dP - delta)
-// then, 32 columns of d at a time,
-//   dV = P^T dO, dK = scale * dS^T Q             (P / dS are the A operands)
-//   dQ = scale * dS K                            (dS transposed through the
-//                                                 wave's own LDS tile)
-// Q, K, dO, V rows are read one row per lane (row = lane % 32, half of D
-// per lane half) for the S / dP products and as 32-float row segments for
-// the others; rows past S are read as row S-1 and carry P = 0.
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_short(BwdArgs a, int nbh)
-{
-    static_assert(D <= 64, "D = 128 takes attn_bwd_short_lds");
-    constexpr int DH = D / 2;
-    constexpr int DB = D / 32;
-    constexpr int TSTR = 36;  // padded row of the 32 x 32 dS tile
-    __shared__ float tiles[kWaves][kBq * TSTR];
-    __shared__ float stats[kWaves][2][kBq];
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h32 = lane >> 5;
-    const int l32 = lane & 31;
-    const int bh = blockIdx.x * kWaves + w;
-    if (bh >= nbh) return;  // no barriers below
-    constexpr int db0 = 0;
-    constexpr int NDB = DB;
-    const int b = bh / a.H;
-    const int hh = bh - b * a.H;
-    const int S = a.S;
-    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
-    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
-    const float *__restrict__ qp = a.q + in_base;
-    const float *__restrict__ kp = a.k + in_base;
-    const float *__restrict__ vp = a.v + in_base;
-    const float *__restrict__ op = a.o + out_base;
-    const float *__restrict__ gp = a.dout + out_base;
-    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
-    auto clampr = [&](int r) { return r < S ? r : S - 1; };
-    float *__restrict__ st = &stats[w][0][0];
-    float *__restrict__ tile = &tiles[w][0];
-
-    // Row statistics: lane (l32, h32) holds half of row l32's <dO, O>; the
-    // halves meet across the lane halves.
-    {
-        const int rc = clampr(l32);
-        float part = 0.0f;
-#pragma unroll
-        for (int c = 0; c < DH; c += 4) {
-            const f32x4 o4 = *(const f32x4 *)(op + rc * out_ss + h32 * DH + c);
-            const f32x4 g4 = *(const f32x4 *)(gp + rc * out_ss + h32 * DH + c);
-            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
-        }
-        part += __shfl_xor(part, 32);
-        if (h32 == 0) {
-            float l2 = INFINITY;
-            if (l32 < S) l2 = a.lse[(int64_t)bh * S + l32] * kLog2e;
-            st[l32] = l2;
-            st[kBq + l32] = l32 < S ? part : 0.0f;
-        }
-    }
-    // This wave's LDS writes land before its reads; the clobber keeps the
-    // compiler from moving memory accesses across.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-
-    // ---- S, dP, then P and dS ----
-    const int rr = clampr(l32);
-    f32x16 sacc = zero16(), pacc = zero16();
-#pragma unroll
-    for (int c = 0; c < DH; c += 4) {
-        const f32x4 q4 = *(const f32x4 *)(qp + rr * in_ss + h32 * DH + c);
-        const f32x4 k4 = *(const f32x4 *)(kp + rr * in_ss + h32 * DH + c);
-        const f32x4 g4 = *(const f32x4 *)(gp + rr * out_ss + h32 * DH + c);
-        const f32x4 v4 = *(const f32x4 *)(vp + rr * in_ss + h32 * DH + c);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sacc = mfma_32x32x2(q4[j], k4[j], sacc);
-            pacc = mfma_32x32x2(g4[j], v4[j], pacc);
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        const int r0 = 8 * g + 4 * h32;  // rows r0 .. r0+3
-        const f32x4 l2 = *(const f32x4 *)&st[r0];
-        const f32x4 dl = *(const f32x4 *)&st[kBq + r0];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = 4 * g + e;
-            float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2[e]));
-            const bool vis = l32 < S && (!CAUSAL || l32 <= r0 + e);
-            p = vis ? p : 0.0f;
-            sacc[i] = p;                     // P
-            pacc[i] = p * (pacc[i] - dl[e]);  // dS
-        }
-    }
-    // dS transposed into this wave's tile: [query][key].
-#pragma unroll
-    for (int i = 0; i < 16; ++i) tile[acc_row(i, h32) * TSTR + l32] = pacc[i];
-
-    // ---- dV, dK ----
-    // The B operands of column block db+1 are loaded before the products of
-    // block db (the scheduling barrier keeps the compiler from issuing each
-    // load just before its MFMA, which would expose one memory latency per
-    // product).
-    float gv[2][16], qv[2][16];
-    auto load_gq = [&](int db, float (&g)[16], float (&q)[16]) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = clampr(acc_row(i, h32));
-            g[i] = gp[r * out_ss + 32 * db + l32];
-            q[i] = qp[r * in_ss + 32 * db + l32];
-        }
-    };
-    load_gq(db0, gv[0], qv[0]);
-#pragma unroll
-    for (int e = 0; e < NDB; ++e) {
-        const int db = db0 + e;
-        if (e + 1 < NDB) load_gq(db + 1, gv[(e + 1) & 1], qv[(e + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-        f32x16 dv = zero16(), dk = zero16();
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            dv = mfma_32x32x2(sacc[i], gv[e & 1][i], dv);
-            dk = mfma_32x32x2(pacc[i], qv[e & 1][i], dk);
-        }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int kr = acc_row(j, h32);
-            if (kr < S) {
-                a.dv[in_base + kr * in_ss + 32 * db + l32] = dv[j];
-                a.dk[in_base + kr * in_ss + 32 * db + l32] = dk[j] * a.scale;
-            }
-        }
-    }
-
-    // ---- dQ: k-step s contracts keys 16*h + s ----
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    float kv[2][16];
-    auto load_k = [&](int db, float (&kk)[16]) {
-#pragma unroll
-        for (int t = 0; t < 16; ++t) kk[t] = kp[clampr(16 * h32 + t) * in_ss + 32 * db + l32];
-    };
-    load_k(db0, kv[0]);
-    f32x4 a4[4];
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) a4[s4] = *(const f32x4 *)&tile[l32 * TSTR + 16 * h32 + 4 * s4];
-#pragma unroll
-    for (int e = 0; e < NDB; ++e) {
-        const int db = db0 + e;
-        if (e + 1 < NDB) load_k(db + 1, kv[(e + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-        f32x16 dq = zero16();
-#pragma unroll
-        for (int t = 0; t < 16; ++t) dq = mfma_32x32x2(a4[t >> 2][t & 3], kv[e & 1][t], dq);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int row = acc_row(j, h32);
-            if (row < S) a.dq[in_base + row * in_ss + 32 * db + l32] = dq[j] * a.scale;
-        }
-    }
-}
-
-// 32 < S <= 64 (D <= 64): one wave per (b, h, key block kb) takes the pairs
-// (qb, kb), qb from kb (causal) or 0 to 1, with the row statistics from
-// attn_bwd_pre's scratch.  dV and dK of the
-// wave's key block are summed over its pairs in registers and stored; dQ of
-// each pair's query block is added with atomics (attn_bwd_pre zeroed it), as
-// the two key blocks' waves both contribute.
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_short2(BwdArgs a, int nbh)
-{
-    static_assert(D <= 64, "S <= 64 kernel: D <= 64");
-    constexpr int DH = D / 2;
-    constexpr int DB = D / 32;
-    constexpr int TSTR = 36;  // padded row of a 32 x 32 dS tile
-    __shared__ float tiles[kWaves][2][kBq * TSTR];
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h32 = lane >> 5;
-    const int l32 = lane & 31;
-    const int item = blockIdx.x * kWaves + w;
-    const int bh = item / 2;
-    if (bh >= nbh) return;  // no barriers below
-    const int kb = item & 1;
-    const int qlo = CAUSAL ? kb : 0;  // pairs (qlo .. 1, kb)
-    const int b = bh / a.H;
-    const int hh = bh - b * a.H;
-    const int S = a.S;
-    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
-    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
-    const float *__restrict__ qp = a.q + in_base;
-    const float *__restrict__ kp = a.k + in_base;
-    const float *__restrict__ vp = a.v + in_base;
-    const float *__restrict__ gp = a.dout + out_base;
-    const float *__restrict__ l2p = a.lse2 + (int64_t)bh * a.S_pad;  // S_pad = 64
-    const float *__restrict__ dlp = a.delta + (int64_t)bh * a.S_pad;
-    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
-    auto clampr = [&](int r) { return r < S ? r : S - 1; };
-
-    // ---- S, dP, P and dS of each pair ----
-    f32x16 pp[2], dd[2];
-    const int key = kBq * kb + l32;
-    const int rk = clampr(key);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int qb = qlo + j;
-        if (qb > 1) break;
-        const int rq = clampr(kBq * qb + l32);
-        f32x16 sacc = zero16(), pacc = zero16();
-#pragma unroll
-        for (int c = 0; c < DH; c += 4) {
-            const f32x4 q4 = *(const f32x4 *)(qp + rq * in_ss + h32 * DH + c);
-            const f32x4 k4 = *(const f32x4 *)(kp + rk * in_ss + h32 * DH + c);
-            const f32x4 g4 = *(const f32x4 *)(gp + rq * out_ss + h32 * DH + c);
-            const f32x4 v4 = *(const f32x4 *)(vp + rk * in_ss + h32 * DH + c);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                sacc = mfma_32x32x2(q4[t], k4[t], sacc);
-                pacc = mfma_32x32x2(g4[t], v4[t], pacc);
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int r0 = kBq * qb + 8 * g + 4 * h32;  // rows r0 .. r0+3 (< S_pad)
-            const f32x4 l2 = *(const f32x4 *)(l2p + r0);
-            const f32x4 dl = *(const f32x4 *)(dlp + r0);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = 4 * g + e;
-                float p = __builtin_amdgcn_exp2f(fmaf(sacc[i], a.c, -l2[e]));
-                const bool vis = key < S && (!CAUSAL || key <= r0 + e);
-                p = vis ? p : 0.0f;
-                sacc[i] = p;
-                pacc[i] = p * (pacc[i] - dl[e]);
-            }
-        }
-        pp[j] = sacc;
-        dd[j] = pacc;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) tiles[w][j][acc_row(i, h32) * TSTR + l32] = pacc[i];
-    }
-
-    // ---- dV, dK of key block kb over the pairs ----
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        f32x16 dv = zero16(), dk = zero16();
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int qb = qlo + j;
-            if (qb > 1) break;
-            float gv[16], qv[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int r = clampr(kBq * qb + acc_row(i, h32));
-                gv[i] = gp[r * out_ss + 32 * db + l32];
-                qv[i] = qp[r * in_ss + 32 * db + l32];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                dv = mfma_32x32x2(pp[j][i], gv[i], dv);
-                dk = mfma_32x32x2(dd[j][i], qv[i], dk);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const int kr = kBq * kb + acc_row(t, h32);
-            if (kr < S) {
-                a.dv[in_base + kr * in_ss + 32 * db + l32] = dv[t];
-                a.dk[in_base + kr * in_ss + 32 * db + l32] = dk[t] * a.scale;
-            }
-        }
-    }
-
-    // ---- dQ of each pair's query block: dS (through LDS) times K[kb] ----
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        float kv[16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) kv[t] = kp[clampr(kBq * kb + 16 * h32 + t) * in_ss + 32 * db + l32];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int qb = qlo + j;
-            if (qb > 1) break;
-            f32x16 dq = zero16();
-#pragma unroll
-            for (int s4 = 0; s4 < 16; s4 += 4) {
-                const f32x4 a4 = *(const f32x4 *)&tiles[w][j][l32 * TSTR + 16 * h32 + s4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) dq = mfma_32x32x2(a4[t], kv[s4 + t], dq);
-            }
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int row = kBq * qb + acc_row(t, h32);
-                if (row < S) unsafeAtomicAdd(a.dq + in_base + (int64_t)row * in_ss + 32 * db + l32, dq[t] * a.scale);
-            }
-        }
-    }
-}
 
 // Short sequences at D = 128 (S <= 32): one workgroup of 4 waves per head,
 // the head's Q, K, V and dO staged in LDS by direct HBM -> LDS copies
@@ -680,6 +372,195 @@ int launch_bwd_short_lds64(const BwdArgs &args, int nbh)
     return launch_ok("attn_bwd_short_lds64") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
+// Short sequences at D <= 64 (S <= R, R = 32 or 64 rows): one workgroup of
+// R/8 waves per head, the head's Q, K, V, dO staged in LDS by direct copies
+// into padded rows (D+4 floats), as attn_bwd_short_lds does at D = 128, but
+// with every product on v_mfma_f32_16x16x4f32 so that the work splits
+// evenly over the waves at any D and R:
+//   wave w: S and dP of the 16 x 16 quadrants w, w + NW, ... of the
+//   (R/16)^2 grid (causal: quadrants above the diagonal are skipped), P and
+//   dS stored transposed ([key][query], rows of R+4) in LDS;
+//   wave w: the 16 x 16 output blocks w, w + NW, ... of dV, dK (rows: keys)
+//   and dQ (rows: queries), 3 (R/16)(D/16) blocks in all, each contracting
+//   16 queries or keys per group of 4 MFMAs (causal: only the groups that
+//   can be nonzero: keys 16rb.. see queries >= 16rb, queries 16rb.. keys
+//   <= 16rb + 15).
+// A 16 x 16 product's A operand [m][k] is lane m + 16k and its B operand
+// [k][n] lane n + 16k: with k = 4 g + j (g = lane / 16, MFMA j of a group
+// of 4), P^T / dS^T rows are read as 128-bit segments, the other operand
+// one float per lane from rows 4 apart (disjoint banks for rows of D+4 or
+// R+4 floats).  R = 32: 46 KB of LDS at D = 64 (three workgroups per CU);
+// R = 64: 104 KB (one per CU).
+template <int D, int R>
+struct LdsBwdShape {
+    static constexpr int NW = R / 8;
+    static constexpr int STR = D + 4;
+    static constexpr int ROWCH = STR / 4;
+    static constexpr int COP = (R * ROWCH + 63) / 64;
+    static constexpr int TILE = COP * 256;
+    static constexpr int PSTR = R + 4;
+    static constexpr int NQ = (R / 16) * (R / 16) / NW;   // quadrants per wave
+    static constexpr int NBO = (R / 16) * (D / 16);        // 16 x 16 blocks per output
+    static constexpr int NB = 3 * NBO / NW;                // output blocks per wave
+    static_assert(NQ * NW == (R / 16) * (R / 16) && NB * NW == 3 * NBO, "even split");
+};
+
+template <int D, int R, bool CAUSAL>
+__global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs a)
+{
+    typedef LdsBwdShape<D, R> L;
+    __shared__ float tiles[4 * L::TILE];  // Q, K, V, dO
+    __shared__ float PT[R * L::PSTR], DT[R * L::PSTR];
+    __shared__ float L2s[R], DLs[R];
+    float *__restrict__ Qs = tiles;
+    float *__restrict__ Ks = tiles + L::TILE;
+    float *__restrict__ Vs = tiles + 2 * L::TILE;
+    float *__restrict__ Gs = tiles + 3 * L::TILE;
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int bh = blockIdx.x;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
+
+    {
+        const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
+        const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
+        const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
+        const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
+#pragma unroll
+        for (int t = w; t < L::COP; t += L::NW) {
+            const int p = 64 * t + lane;
+            int r = p / L::ROWCH;
+            const int c = p - r * L::ROWCH;
+            const bool real = r < R && c < D / 4;
+            r = r < S ? r : S - 1;
+            const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
+            const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
+            dma16_buf(rq, oi, Qs + 256 * t);
+            dma16_buf(rk, oi, Ks + 256 * t);
+            dma16_buf(rv, oi, Vs + 256 * t);
+            dma16_buf(rg, og, Gs + 256 * t);
+        }
+    }
+    // Row statistics of rows 8w..8w+7, 8 lanes per row.
+    {
+        constexpr int CH = D / 32;  // 16-byte chunks per lane
+        const int j = 8 * w + (lane >> 3);
+        const int s8 = lane & 7;
+        const int jr = j < S ? j : S - 1;
+        const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
+        const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
+        float part = 0.0f;
+#pragma unroll
+        for (int it = 0; it < CH; ++it) {
+            const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
+            const f32x4 g4 = *(const f32x4 *)(grow + 32 * it + 4 * s8);
+            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
+        }
+        part += __shfl_xor(part, 1);
+        part += __shfl_xor(part, 2);
+        part += __shfl_xor(part, 4);
+        if (s8 == 0) {
+            L2s[j] = j < S ? a.lse[(int64_t)bh * S + j] * kLog2e : INFINITY;
+            DLs[j] = j < S ? part : 0.0f;
+        }
+    }
+    wait_vmem();
+    __syncthreads();
+
+    const int l16 = lane & 15, g4 = lane >> 4;
+    // ---- S, dP, P, dS of this wave's quadrants ----
+#pragma unroll
+    for (int u = 0; u < L::NQ; ++u) {
+        const int quad = w + L::NW * u;
+        const int qm = quad / (R / 16), qn = quad - qm * (R / 16);
+        const int key = 16 * qn + l16;
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+        if (!CAUSAL || qn <= qm) {
+            const int arow = (16 * qm + l16) * L::STR + 4 * g4;
+            const int brow = key * L::STR + 4 * g4;
+#pragma unroll
+            for (int c0 = 0; c0 < D; c0 += 16) {
+                const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
+                const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
+                const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
+                const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[j], kf[j], sacc, 0, 0, 0);
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[j], vf[j], pacc, 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int qi = 16 * qm + 4 * g4 + r;
+            float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
+            const bool vis = key < S && (!CAUSAL || key <= qi);
+            p = vis ? p : 0.0f;
+            PT[key * L::PSTR + qi] = p;
+            DT[key * L::PSTR + qi] = p * (pacc[r] - DLs[qi]);
+        }
+    }
+    __syncthreads();
+
+    // ---- this wave's 16 x 16 blocks of dV, dK, dQ ----
+#pragma unroll
+    for (int u = 0; u < L::NB; ++u) {
+        const int blk = w + L::NW * u;
+        const int o = blk / L::NBO;  // 0 dV, 1 dK, 2 dQ
+        const int rem = blk - o * L::NBO;
+        const int rb = rem / (D / 16), cb = rem - rb * (D / 16);
+        const int col = 16 * cb + l16;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (o < 2) {
+            // dV[k][n] = sum_q P^T[k][q] dO[q][n];  dK[k][n] = sum_q dS^T[k][q] Q[q][n]
+            const float *__restrict__ A = o == 0 ? PT : DT;
+            const float *__restrict__ Bt = o == 0 ? Gs : Qs;
+#pragma unroll
+            for (int c = 0; c < R / 16; ++c) {
+                if (CAUSAL && c < rb) continue;
+                const f32x4 af = *(const f32x4 *)&A[(16 * rb + l16) * L::PSTR + 16 * c + 4 * g4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[j], Bt[(16 * c + 4 * g4 + j) * L::STR + col],
+                                                              acc, 0, 0, 0);
+            }
+        } else {
+            // dQ[m][n] = sum_k dS[m][k] K[k][n] = sum_k dS^T[k][m] K[k][n]
+#pragma unroll
+            for (int c = 0; c < R / 16; ++c) {
+                if (CAUSAL && c > rb) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int kk = 16 * c + 4 * g4 + j;
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(DT[kk * L::PSTR + 16 * rb + l16],
+                                                              Ks[kk * L::STR + col], acc, 0, 0, 0);
+                }
+            }
+        }
+        float *__restrict__ dst = o == 0 ? a.dv : (o == 1 ? a.dk : a.dq);
+        const float mul = o == 0 ? 1.0f : a.scale;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * rb + 4 * g4 + r;
+            if (row < S) dst[in_base + (int64_t)row * in_ss + col] = acc[r] * mul;
+        }
+    }
+}
+
+template <int D, int R, bool CAUSAL>
+int launch_bwd_lds16(const BwdArgs &args, int nbh)
+{
+    hipLaunchKernelGGL((attn_bwd_lds16<D, R, CAUSAL>), dim3((unsigned)nbh), dim3(R * 8), 0, 0, args);
+    return launch_ok("attn_bwd_lds16") ? EMBER_OK : EMBER_ERR_DEVICE;
+}
+
 template <bool CAUSAL>
 int launch_bwd_short_lds(const BwdArgs &args, int nbh)
 {
@@ -687,25 +568,6 @@ int launch_bwd_short_lds(const BwdArgs &args, int nbh)
     return launch_ok("attn_bwd_short_lds") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
-template <int D, bool CAUSAL>
-int launch_bwd_short2(const BwdArgs &args, int64_t rows_pad, int nbh)
-{
-    constexpr int RPB = 256 / (D / 4);
-    const int pre_blocks = (int)((rows_pad + RPB - 1) / RPB);
-    hipLaunchKernelGGL((attn_bwd_pre<D>), dim3(pre_blocks), dim3(256), 0, 0, args, rows_pad);
-    if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
-    const dim3 grid((unsigned)(((int64_t)nbh * 2 + kWaves - 1) / kWaves));
-    hipLaunchKernelGGL((attn_bwd_short2<D, CAUSAL>), grid, dim3(kThreads), 0, 0, args, nbh);
-    return launch_ok("attn_bwd_short2") ? EMBER_OK : EMBER_ERR_DEVICE;
-}
-
-template <int D, bool CAUSAL>
-int launch_bwd_short(const BwdArgs &args, int nbh)
-{
-    const dim3 grid((unsigned)(((int64_t)nbh + kWaves - 1) / kWaves));
-    hipLaunchKernelGGL((attn_bwd_short<D, CAUSAL>), grid, dim3(kThreads), 0, 0, args, nbh);
-    return launch_ok("attn_bwd_short") ? EMBER_OK : EMBER_ERR_DEVICE;
-}
 
 }  // namespace
 }  // namespace ember
@@ -769,11 +631,15 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, who);
     if (st != EMBER_OK || B * H * S == 0) return st;
 
-    // S <= 32: one wave per head at D <= 64 (attn_bwd_short; measured
-    // 1.5-3x the workgroup kernel's throughput there) and one LDS-staged
-    // workgroup per head at D = 128 (attn_bwd_short_lds: 4.8 TB/s at S = 32,
-    // against 2.8 for two register-fed waves per head).
-    if (S <= kBq) {
+    // S <= 64: one workgroup per head with its Q, K, V and dO staged in LDS,
+    // the row statistics formed in the kernel (no scratch, no atomics):
+    // attn_bwd_short_lds (S <= 32) and attn_bwd_short_lds64 at D = 128,
+    // attn_bwd_lds16 with 32- or 64-row tiles at D <= 64.  Measured with
+    // 2^20 query rows: 4.6-4.9 TB/s at S = 32 and 3.2-3.6 TB/s at S = 64,
+    // where the register-fed kernels they replaced (one wave per head or
+    // per key block, rows read one per lane from HBM) moved 2.8-3.5 and
+    // 2.0-2.1 TB/s.
+    if (S <= 2 * kBq) {
         BwdArgs sa;
         sa.q = q;
         sa.k = k;
@@ -797,42 +663,21 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
         sa.out_sh = out_sh;
         sa.out_ss = out_ss;
         const int nbh = (int)(B * H);
-        switch (D * 2 + (causal ? 1 : 0)) {
-            case 64: return launch_bwd_short<32, false>(sa, nbh);
-            case 65: return launch_bwd_short<32, true>(sa, nbh);
-            case 128: return launch_bwd_short<64, false>(sa, nbh);
-            case 129: return launch_bwd_short<64, true>(sa, nbh);
-            case 256: return launch_bwd_short_lds<false>(sa, nbh);
-            default: return launch_bwd_short_lds<true>(sa, nbh);
+        const int key = (S <= kBq ? 0 : 8) + (int)(D / 32) * 2 + (causal ? 1 : 0);
+        switch (key) {
+            case 2: return launch_bwd_lds16<32, 32, false>(sa, nbh);
+            case 3: return launch_bwd_lds16<32, 32, true>(sa, nbh);
+            case 4: return launch_bwd_lds16<64, 32, false>(sa, nbh);
+            case 5: return launch_bwd_lds16<64, 32, true>(sa, nbh);
+            case 8: return launch_bwd_short_lds<false>(sa, nbh);
+            case 9: return launch_bwd_short_lds<true>(sa, nbh);
+            case 10: return launch_bwd_lds16<32, 64, false>(sa, nbh);
+            case 11: return launch_bwd_lds16<32, 64, true>(sa, nbh);
+            case 12: return launch_bwd_lds16<64, 64, false>(sa, nbh);
+            case 13: return launch_bwd_lds16<64, 64, true>(sa, nbh);
+            case 16: return launch_bwd_short_lds64<false>(sa, nbh);
+            default: return launch_bwd_short_lds64<true>(sa, nbh);
         }
-    }
-    // 32 < S <= 64 at D = 128: one 8-wave workgroup per head, LDS-staged
-    // (attn_bwd_short_lds64); like the S <= 32 kernels it needs no scratch.
-    if (S <= 2 * kBq && D == 128) {
-        BwdArgs sa;
-        sa.q = q;
-        sa.k = k;
-        sa.v = v;
-        sa.o = o;
-        sa.lse = lse;
-        sa.dout = d_o;
-        sa.dq = dq;
-        sa.dk = dk;
-        sa.dv = dv;
-        sa.lse2 = sa.delta = nullptr;
-        sa.H = (int)H;
-        sa.S = (int)S;
-        sa.S_pad = sa.nkb = 0;
-        sa.c = scale * kLog2e;
-        sa.scale = scale;
-        sa.in_sb = in_sb;
-        sa.in_sh = in_sh;
-        sa.in_ss = in_ss;
-        sa.out_sb = out_sb;
-        sa.out_sh = out_sh;
-        sa.out_ss = out_ss;
-        return causal ? launch_bwd_short_lds64<true>(sa, (int)(B * H))
-                      : launch_bwd_short_lds64<false>(sa, (int)(B * H));
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
@@ -865,17 +710,6 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.out_sh = out_sh;
     args.out_ss = out_ss;
     const int nblocks = args.nkb * (int)(B * H);
-    // 32 < S <= 64 at D <= 64: one wave per (head, key block) (measured
-    // +2 to +58 % over the workgroup kernel; at D = 128, two waves per key
-    // block measured -17 to +17 %, so D = 128 stays with the workgroup kernel).
-    if (S <= 2 * kBq && D <= 64) {
-        switch (D * 2 + (causal ? 1 : 0)) {
-            case 64: return launch_bwd_short2<32, false>(args, rows_pad, (int)(B * H));
-            case 65: return launch_bwd_short2<32, true>(args, rows_pad, (int)(B * H));
-            case 128: return launch_bwd_short2<64, false>(args, rows_pad, (int)(B * H));
-            default: return launch_bwd_short2<64, true>(args, rows_pad, (int)(B * H));
-        }
-    }
     switch (D * 2 + (causal ? 1 : 0)) {
         case 64: return launch_bwd<32, false>(args, rows_pad, nblocks);
         case 65: return launch_bwd<32, true>(args, rows_pad, nblocks);

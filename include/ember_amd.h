@@ -145,11 +145,11 @@ int attention_fwd(const float *q, const float *k, const float *v, float *o, floa
  * upstream gradient d_o, writes dq, dk, dv (same layout as q, k, v).  P is
  * recomputed from lse; the S x S matrix is never stored.  Needs
  * 2*B*H*S_pad*4 bytes of device scratch (S_pad = S rounded up to 32; none at
- * S <= 32), which the library keeps cached between calls.
- * Determinism: dk and dv are bitwise reproducible.  For S > 32, dq is
+ * S <= 64), which the library keeps cached between calls.
+ * Determinism: dk and dv are bitwise reproducible.  For S > 64, dq is
  * accumulated in HBM with fp32 atomic adds from every key block that sees a
  * query row, so its last bits vary from run to run (each run within the
- * stated tolerance); at S <= 32 it is reproducible too.  Because of those
+ * stated tolerance); at S <= 64 it is reproducible too.  Because of those
  * atomics dq must be device memory (not host or managed memory), and dq must
  * not overlap q, k, v, o, lse, d_o, dk or dv. */
 int attention_bwd(const float *q, const float *k, const float *v, const float *o,
@@ -166,7 +166,8 @@ int attention_bwd(const float *q, const float *k, const float *v, const float *o
  * array inside the library, one per GPU, held until the process ends, instead
  * of library-allocated scratch.  Limit: B*H*S_pad <= 2^21 rows (S_pad = S
  * rounded up to 32); a larger call returns EMBER_ERR_INVALID_ARGUMENT and
- * launches nothing.  Every call on one GPU shares that GPU's array.  Calls
+ * launches nothing (S <= 64 needs no statistics and so no array space).
+ * Every call on one GPU shares that GPU's array.  Calls
  * are ordered because all library work runs on the null stream; launches of
  * this entry point that overlap on one GPU (for example replayed on several
  * streams at once) race on the array.  Each call writes every statistic it
