@@ -32,6 +32,8 @@
 // applied only on tiles that cross the diagonal or the sequence end.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "lds_dma.h"
 #include "mfma.h"
@@ -75,11 +77,11 @@ template <int D> struct FwdTile {
 //   copy K(t+1) -> Ks;  O^T += V^T . P^T
 // A wave whose queries all precede the tile (causal) skips the products
 // but still issues its copies and meets both barriers.
-// Workgroups per CU: two, or three for non-causal D = 64 (LDS fits three
-// at D = 64; measured, the causal kernel runs best with two and the
-// non-causal one with three).
+// Workgroups per CU: two, or three at D = 64 (LDS fits three there; the
+// causal D = 64 kernel fits three in registers thanks to its split loop,
+// see the end of the kernel).
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd_kernel(FwdArgs a)
+__global__ __launch_bounds__(kThreads, D == 64 ? 3 : 2) void attn_fwd_kernel(FwdArgs a)
 {
     typedef FwdTile<D> T;
     constexpr int DH = D / 2;   // contraction length per lane half (k-steps)
@@ -209,12 +211,13 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
     float mrun = -INFINITY;  // reference max of s*c for query mq (see below)
     float lrun = 0.0f;       // this lane half's share of the running sum
 
-    for (int t = 0; t < ntiles; ++t) {
+    auto tile = [&](int t, auto masked) {
+        constexpr bool MASKED = decltype(masked)::value;
         const int n0 = t * kBc;
         wait_vmem();      // this wave's copies of K tile t have landed
         __syncthreads();  // all of K tile t is in LDS; every wave is done with Vs
         fetch_v(n0);
-        const bool active = !(CAUSAL && n0 > m0 + 31);  // some key at or before a query
+        const bool active = !MASKED || !(CAUSAL && n0 > m0 + 31);  // some key at or before a query
         f32x16 sacc[kBc / 32];
         if (active) {
             // S^T = K . Q^T for two 32-key blocks.
@@ -231,7 +234,7 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
             }
 
             // Mask (diagonal and tail tiles only), tile max of the raw scores.
-            const bool need_mask = (n0 + kBc > S) || (CAUSAL && n0 + kBc - 1 > m0);
+            const bool need_mask = MASKED && ((n0 + kBc > S) || (CAUSAL && n0 + kBc - 1 > m0));
             if (need_mask) {
 #pragma unroll
                 for (int blk = 0; blk < kBc / 32; ++blk) {
@@ -304,7 +307,19 @@ __global__ __launch_bounds__(kThreads, D == 64 && !CAUSAL ? 3 : 2) void attn_fwd
                 }
             }
         }
+    };
+    // Causal D = 64: the tiles wholly before the workgroup's first query need
+    // no mask for any wave and run a mask-free copy of the loop body; with
+    // only the last (diagonal) tiles carrying the mask the kernel fits three
+    // workgroups per CU without spilling (146 VGPRs; one loop with the mask
+    // test inside needed 178, or spilled 8-10 at three per CU).  Measured:
+    // +1 % at config 2, +3 % at S = 4096.  The other instantiations keep one
+    // loop (splitting measured -1 % at D = 128 and -2 % for non-causal D = 64).
+    int t = 0;
+    if constexpr (D == 64 && CAUSAL) {
+        for (const int nfull = min(q0 / kBc, ntiles); t < nfull; ++t) tile(t, std::false_type{});
     }
+    for (; t < ntiles; ++t) tile(t, std::true_type{});
 
     const float ltot = lrun + __shfl_xor(lrun, 32);
     if (mq < S) {

@@ -9,7 +9,9 @@ The first sweep keeps B, H <= 3, so its launches with S > 64 are small
 S <= 64 they take the packed and wave forwards and the short backwards.  The
 second sweep draws enough heads that ceil(S/128) * B * H > 64, which sends
 the forward to the one-head-per-workgroup kernel (attn_fwd_kernel) on the
-same kind of padded strides.  Tolerance as everywhere: max-abs 2e-4 /
+same kind of padded strides.  The third keeps S <= 64 (the backward's
+LDS-staged one-workgroup-per-head kernels) with 20-640 heads, so that
+several workgroups share each CU.  Tolerance as everywhere: max-abs 2e-4 /
 rel 1e-3; padding must stay untouched.
 """
 
@@ -35,6 +37,19 @@ def _case(seed):
     causal = bool(rng.integers(0, 2))
     pads = [int(rng.choice([0, 4, 12, 32])) for _ in range(2)]  # row padding (floats) per triple
     hpads = [int(rng.choice([0, 1, 3])) for _ in range(2)]       # extra rows per head per triple
+    return B, H, S, D, causal, pads, hpads
+
+
+def _short_case(seed):
+    """S <= 64 (the LDS-staged one-workgroup-per-head backward kernels) with
+    enough heads that several workgroups share each CU."""
+    rng = np.random.default_rng(40_000 + seed)
+    B, H = int(rng.integers(1, 9)), int(rng.integers(20, 80))
+    S = int(rng.choice([1, 3, 16, 17, 31, 32, 33, 40, 47, 63, 64]))
+    D = int(rng.choice([32, 64, 128]))
+    causal = bool(rng.integers(0, 2))
+    pads = [int(rng.choice([0, 4, 12, 32])) for _ in range(2)]
+    hpads = [int(rng.choice([0, 1, 3])) for _ in range(2)]
     return B, H, S, D, causal, pads, hpads
 
 
@@ -83,6 +98,11 @@ def test_random_shape_and_layout(seed):
 @pytest.mark.parametrize("seed", range(12))
 def test_random_wide_launch_and_layout(seed):
     _run(100 + seed, *_wide_case(seed))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_short_sequence_many_heads(seed):
+    _run(200 + seed, *_short_case(seed))
 
 
 def _run(seed, B, H, S, D, causal, pads, hpads):
