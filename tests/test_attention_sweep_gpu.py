@@ -105,6 +105,20 @@ def test_random_short_sequence_many_heads(seed):
     _run(200 + seed, *_short_case(seed))
 
 
+@pytest.mark.parametrize("B,H,S,causal,pads,hpads", [
+    (1, 257, 32, False, [0, 0], [0, 0]),
+    (3, 171, 9, True, [4, 12], [1, 0]),
+    (5, 206, 32, True, [0, 32], [3, 1]),
+    (8, 128, 32, False, [12, 4], [0, 3]),
+    (16, 160, 31, False, [0, 0], [0, 0]),
+])
+def test_short_backward_walks_many_heads(B, H, S, causal, pads, hpads):
+    """S <= 32 at D = 128 with hundreds to thousands of one-head workgroups
+    (257 to 2560 heads, ragged S), padded strides on both triples: the
+    workgroups that share a CU must not disturb each other's LDS tiles."""
+    _run(300 + B + H + S, B, H, S, 128, causal, pads, hpads)
+
+
 def _run(seed, B, H, S, D, causal, pads, hpads):
     G.say(f"sweep seed={seed} B={B} H={H} S={S} D={D} causal={causal} pads={pads} hpads={hpads}")
     rng = np.random.default_rng(seed)
