@@ -349,7 +349,7 @@ def secondary(L, ev):
     out, keep = {}, {}
     rng = np.random.default_rng(5)
 
-    def attn(tag, B, H, S, D, causal, bwd, reps, kept=False):
+    def attn(tag, B, H, S, D, causal, bwd, reps, kept=False, det=False):
         n = B * H * S * D
         hosts = [rng.standard_normal(n, dtype=np.float32) for _ in range(3)]
         q, k, v = (DeviceArray((n,), h) for h in hosts)
@@ -371,6 +371,15 @@ def secondary(L, ev):
             rec.update(bwd_ms=round(bwd_ms, 4), bwd_tflops=round(bwd_fl / bwd_ms / 1e9, 2),
                        fwd_bwd_tflops=round((fwd_fl + bwd_fl) / (fwd_ms + bwd_ms) / 1e9, 2),
                        bwd_hbm_gbs=round((32 * n + 8 * B * H * S) / bwd_ms / 1e6, 1))
+            if det:  # the same backward with ember_set_deterministic(1)
+                L.ember_set_deterministic(1)
+                try:
+                    det_ms = _timed(ev, b, reps)
+                finally:
+                    L.ember_set_deterministic(0)
+                rec.update(bwd_deterministic_ms=round(det_ms, 4),
+                           bwd_deterministic_tflops=round(bwd_fl / det_ms / 1e9, 2),
+                           deterministic_time_ratio=round(det_ms / bwd_ms, 3))
         fwd_bytes = 16 * B * H * S * D + 4 * B * H * S
         rec["fwd_hbm_gbs"] = round(fwd_bytes / fwd_ms / 1e6, 1)
         capi.check(what=tag)
@@ -380,13 +389,16 @@ def secondary(L, ev):
 
     attn("config1_fwd", 1, 4, 256, 64, False, False, 50, kept=True)
     attn("config2_causal_fwd", 8, 16, 2048, 64, True, False, 20, kept=True)
-    attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20)
+    attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20, det=True)
+    # Config 3's backward once more in deterministic mode (dq partials:
+    # 8 GiB of scratch, released right after).
+    attn("config3_deterministic_bwd", 4, 32, 4096, 128, True, True, 5, det=True)
+    L.ember_empty_cache()
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
-    # The backward where it is HBM-bound (AI = S/8 causal): S = 32 (one wave
-    # per head at D = 64, one LDS-staged workgroup per head at D = 128),
-    # S = 64 (one wave per key block at D = 64, the workgroup kernel at
-    # D = 128) and S = 128 (the workgroup kernel).
+    # The backward where it is HBM-bound (AI = S/8 causal): S = 32 and 64
+    # (one LDS-staged workgroup per head) and S = 128 (the key-block
+    # workgroup kernel).
     for S in (32, 64, 128):
         for D in (64, 128):
             attn(f"short_s{S}_d{D}_fwd_bwd", (1 << 20) // S // 64, 64, S, D, True, True, 20)

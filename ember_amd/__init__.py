@@ -16,14 +16,17 @@ _TENSOR_NAMES = (
     "tanh", "ctgh", "T", "sum", "softmax", "sqrt", "attention", "attention_forward",
     "attention_backward", "synchronize", "empty_cache", "memory_stats",
 )
+_CAPI_NAMES = ("set_deterministic", "is_deterministic")
 _SUBMODULES = ("nn", "optim", "loss", "random", "capi", "build")
 
-__all__ = list(_TENSOR_NAMES) + ["nn", "optim", "loss", "random"]
+__all__ = list(_TENSOR_NAMES) + list(_CAPI_NAMES) + ["nn", "optim", "loss", "random"]
 
 
 def __getattr__(name: str):
     if name in _TENSOR_NAMES:
         return getattr(importlib.import_module("ember_amd.tensor"), name)
+    if name in _CAPI_NAMES:
+        return getattr(importlib.import_module("ember_amd.capi"), name)
     if name in _SUBMODULES:
         return importlib.import_module(f"ember_amd.{name}")
     raise AttributeError(f"module 'ember_amd' has no attribute {name!r}")

@@ -81,10 +81,27 @@ def lib() -> C.CDLL:
     L.softmax_axis.argtypes = [_vp, _vp, C.c_int, C.c_int, C.c_int]
     L.gemm_ex.restype = C.c_int
     L.gemm_ex.argtypes = [_vp] * 3 + [C.c_int] * 6 + [_vp] * 3 + [C.c_int]
+    L.ember_set_deterministic.argtypes = [C.c_int]
+    L.ember_set_deterministic.restype = None
+    L.ember_get_deterministic.argtypes = []
+    L.ember_get_deterministic.restype = C.c_int
     L.adam_step.restype = C.c_int
     L.adam_step.argtypes = [C.POINTER(_vp)] * 4 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 4 + [_i64]
     _lib = L
     return L
+
+
+def set_deterministic(enabled: bool) -> None:
+    """Process-wide switch for bitwise-reproducible results
+    (ember_set_deterministic).  Off by default.  With it on, attention_bwd's
+    dq at S > 64 is summed in a fixed key order (a scratch buffer of
+    ceil(S/128)*B*H*S_pad*128 floats and one extra pass) instead of with
+    atomic adds; every other operator is reproducible either way."""
+    lib().ember_set_deterministic(1 if enabled else 0)
+
+
+def is_deterministic() -> bool:
+    return bool(lib().ember_get_deterministic())
 
 
 def check(status: int | None = None, what: str = "ember_amd") -> None:

@@ -624,7 +624,7 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
                        const float *lse, const float *d_o, float *dq, float *dk, float *dv, int64_t B,
                        int64_t H, int64_t S, int64_t D, float scale, int causal, int64_t in_sb,
                        int64_t in_sh, int64_t in_ss, int64_t out_sb, int64_t out_sh, int64_t out_ss,
-                       StatsSource stats_source, const char *who)
+                       StatsSource stats_source, bool noalloc, const char *who)
 {
     const void *ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv};
     const int64_t strides[] = {in_sb, in_sh, in_ss, out_sb, out_sh, out_ss};
@@ -650,7 +650,7 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
         sa.dq = dq;
         sa.dk = dk;
         sa.dv = dv;
-        sa.lse2 = sa.delta = nullptr;
+        sa.lse2 = sa.delta = sa.dq_part = nullptr;
         sa.H = (int)H;
         sa.S = (int)S;
         sa.S_pad = sa.nkb = 0;
@@ -681,6 +681,22 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
+    const int64_t nkb = (S + kBk - 1) / kBk;
+    // Deterministic dq: per-key-block partials, summed in a fixed order.
+    float *dq_part = nullptr;
+    if (deterministic()) {
+        if (noalloc)
+            return record_error(EMBER_ERR_UNSUPPORTED,
+                                "attention_bwd_noalloc: deterministic dq at S > 64 needs a scratch "
+                                "buffer (use attention_bwd)");
+        // B*H*S_pad*128*4 < 2^61 (B*H < 2^21, S < 2^30): the product below
+        // cannot wrap once nkb passes this check.
+        if (nkb > INT64_MAX / (B * H * S_pad * kBk * (int64_t)sizeof(float)))
+            return record_error(EMBER_ERR_OUT_OF_MEMORY, "attention_bwd: deterministic dq partials");
+        dq_part = (float *)scratch(kScratchAttnDqPart,
+                                   (size_t)dq_part_floats(nkb, B * H, S_pad) * sizeof(float));
+        if (!dq_part) return EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
+    }
     float *stats = nullptr;
     st = stats_source(rows_pad, &stats);
     if (st != EMBER_OK) return st;
@@ -697,10 +713,11 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.dv = dv;
     args.lse2 = stats;
     args.delta = stats + rows_pad;
+    args.dq_part = dq_part;
     args.H = (int)H;
     args.S = (int)S;
     args.S_pad = (int)S_pad;
-    args.nkb = (int)((S + kBk - 1) / kBk);
+    args.nkb = (int)nkb;
     args.c = scale * kLog2e;
     args.scale = scale;
     args.in_sb = in_sb;
@@ -731,7 +748,7 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
 {
     return ember::attention_bwd_rows(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale, causal, in_sb,
                                      in_sh, in_ss, out_sb, out_sh, out_ss, ember::library_stats,
-                                     "attention_bwd");
+                                     false, "attention_bwd");
 }
 
 // The same computation with the row statistics in the fixed array above:
@@ -750,5 +767,5 @@ extern "C" int attention_bwd_noalloc(const float *q, const float *k, const float
 {
     return ember::attention_bwd_rows(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale, causal, in_sb,
                                      in_sh, in_ss, out_sb, out_sh, out_ss, ember::noalloc_stats,
-                                     "attention_bwd_noalloc");
+                                     true, "attention_bwd_noalloc");
 }

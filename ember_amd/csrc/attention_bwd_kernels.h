@@ -24,6 +24,9 @@
 //     dS of all 4 waves goes through LDS so that dQ(32 x D) = dS . K over the
 //     workgroup's 128 keys is one more MFMA product per wave, added to the
 //     global dQ with hardware fp32 atomics (dq must be device memory).
+//     Deterministic mode (ember_set_deterministic) instead stores each
+//     wave's dQ contribution into a partial slab of its own, and a third
+//     launch (attn_bwd_dq_reduce) sums the slabs in ascending key order.
 //     That product is software-pipelined by one block: block j's step runs
 //     the dQ MFMAs of block j-1 in between block j's softmax instructions,
 //     so the matrix core keeps working while the softmax's VALU and
@@ -62,6 +65,10 @@ struct BwdArgs {
     const float *q, *k, *v, *o, *lse, *dout;
     float *dq, *dk, *dv;
     float *lse2, *delta;  // row statistics, (B*H, S_pad) each
+    // Deterministic mode (ember_set_deterministic): dq contributions, one
+    // dense (B*H, S_pad, D) slab per 128 / NSPLIT keys (attn_bwd_dq_reduce
+    // sums them); null otherwise (dq accumulated with atomics).
+    float *dq_part;
     int H, S, S_pad, nkb;
     float c;      // scale * log2(e)
     float scale;
@@ -111,8 +118,10 @@ __global__ __launch_bounds__(256) void attn_bwd_pre(BwdArgs a, int64_t rows_pad)
         a.delta[row] = s;
         a.lse2[row] = a.lse[bh * a.S + m] * kLog2e;
     }
-    const int64_t qoff = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub;
-    *(f32x4 *)(a.dq + qoff) = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!a.dq_part) {  // deterministic mode: attn_bwd_dq_reduce writes all of dq
+        const int64_t qoff = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub;
+        *(f32x4 *)(a.dq + qoff) = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 }
 
 template <int D>
@@ -139,7 +148,7 @@ constexpr int kMaxSlots = 5;  // BwdLayout<128>::SLOTS
 struct BwdBlock {
     const float *qp, *gp;      // q, dO at (b, h)
     const float *l2p, *dlp;    // lse2, delta at (b, h)
-    float *dqp;                // dq at (b, h)
+    float *dqp;                // dq at (b, h); deterministic: this wave's dq_part slab at (b, h)
     int S, nq, n0w, w;
     int in_ss, out_ss;
     // Per copy slot s (copy t = w + 4s of a tile): this lane's chunk as a
@@ -233,8 +242,10 @@ __device__ __forceinline__ DqState<D> dq_state(int w)
     return st;
 }
 
-// Adds the finished dQ block (rows m0..m0+31) to global memory.
-template <int D>
+// Adds the finished dQ block (rows m0..m0+31) to global memory, or (DET)
+// stores it into this wave's partial slab: dense rows of D floats, all 32
+// rows (the slab has S_pad rows; rows past S hold zeros and are never read).
+template <int D, bool DET>
 __device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, int m0, const f32x16 &qacc)
 {
     constexpr int DB = BwdLayout<D>::DB;
@@ -242,6 +253,12 @@ __device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, in
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
     const int dblk = k.w % DB;
+    if constexpr (DET) {
+        float *pb = k.dqp + (int64_t)m0 * D + 32 * dblk + 4 * h32 * D + l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pb[((i >> 2) * 8 + (i & 3)) * D] = qacc[i] * a.scale;
+        return;
+    }
     // Row i of the block: wave-uniform row base + unsigned lane offset.
     float *dqb = k.dqp + (int64_t)m0 * k.in_ss + 32 * dblk;
     const unsigned qoff = (unsigned)(4 * h32 * k.in_ss + l32);
@@ -297,7 +314,7 @@ __device__ __forceinline__ void dq_softmax(const BwdArgs &a, const float *__rest
 //   3. the dQ product of block qb-1 (dS in LDS since the last barrier),
 //      interleaved with the softmax of block qb: its VALU work issues while
 //      the dQ MFMAs run, instead of leaving the matrix core idle;
-//   4. dQ of block qb-1 to global memory (atomics);
+//   4. dQ of block qb-1 to global memory (atomics; DET: partial stores);
 //   5. dV += P^T dO, dK += dS^T Q of block qb;
 //   6. barrier (every wave has read dS of block qb-1), dS of block qb to
 //      LDS, wait for the copies, barrier.
@@ -305,7 +322,7 @@ __device__ __forceinline__ void dq_softmax(const BwdArgs &a, const float *__rest
 // per-lane threshold), so steps 2 and 3 are one basic block.  Keys a wave
 // cannot see in this block (causal, above the diagonal) get P = 0 by the same
 // compare, so no wave skips the block.
-template <int D, bool CAUSAL, bool PREV, bool MASK>
+template <int D, bool CAUSAL, bool PREV, bool MASK, bool DET>
 __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, int qb,
                                          const float *__restrict__ qs,
                                          const float *__restrict__ gs,
@@ -370,7 +387,7 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
             pacc[i] = y;
         }
     }
-    if (PREV) dq_store<D>(a, k, m0 - kBq, qacc);
+    if (PREV) dq_store<D, DET>(a, k, m0 - kBq, qacc);
 
     // ---- dV += P^T dO, dK += dS^T Q ----
     {
@@ -400,7 +417,7 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
 }
 
 // dQ of the last block (its dS is in LDS after the last step's barrier).
-template <int D>
+template <int D, bool DET>
 __device__ __forceinline__ void bwd_last_dq(const BwdArgs &a, const BwdBlock &k, int m0,
                                             const float *__restrict__ ds,
                                             const float *__restrict__ kall)
@@ -414,10 +431,10 @@ __device__ __forceinline__ void bwd_last_dq(const BwdArgs &a, const BwdBlock &k,
 #pragma unroll
         for (int j = 0; j < 4; ++j) qacc = mfma_32x32x2(sf[j], kall[dqs.kbase + (kk + j) * D], qacc);
     }
-    dq_store<D>(a, k, m0, qacc);
+    dq_store<D, DET>(a, k, m0, qacc);
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool DET>
 __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
 {
     typedef BwdLayout<D> L;
@@ -454,7 +471,10 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     k.gp = a.dout + out_base;
     k.l2p = a.lse2 + (int64_t)bh * a.S_pad;
     k.dlp = a.delta + (int64_t)bh * a.S_pad;
-    k.dqp = a.dq + in_base;
+    if constexpr (DET)
+        k.dqp = a.dq_part + ((int64_t)(kb * L::NSPLIT + w / DB) * BH + bh) * a.S_pad * D;
+    else
+        k.dqp = a.dq + in_base;
     k.S = S;
     k.nq = (S + kBq - 1) / kBq;
     k.w = w;
@@ -520,21 +540,21 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     const int tail_bias = k.n0w + l32 >= S ? (1 << 24) : 0;
     auto walk = [&](auto mask) {
         constexpr bool M = decltype(mask)::value;
-        bwd_step<D, CAUSAL, false, M>(a, k, qstart, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1, Kall, kr,
-                                      vr, dvacc, dkacc, tail_bias);
+        bwd_step<D, CAUSAL, false, M, DET>(a, k, qstart, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1, Kall,
+                                           kr, vr, dvacc, dkacc, tail_bias);
         for (int qb = qstart + 1; qb < k.nq; qb += 2) {
-            bwd_step<D, CAUSAL, true, M>(a, k, qb, Qs1, dOs1, St1, dSs, Qs0, dOs0, St0, Kall, kr,
-                                         vr, dvacc, dkacc, tail_bias);
+            bwd_step<D, CAUSAL, true, M, DET>(a, k, qb, Qs1, dOs1, St1, dSs, Qs0, dOs0, St0, Kall,
+                                              kr, vr, dvacc, dkacc, tail_bias);
             if (qb + 1 < k.nq)
-                bwd_step<D, CAUSAL, true, M>(a, k, qb + 1, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1,
-                                             Kall, kr, vr, dvacc, dkacc, tail_bias);
+                bwd_step<D, CAUSAL, true, M, DET>(a, k, qb + 1, Qs0, dOs0, St0, dSs, Qs1, dOs1,
+                                                  St1, Kall, kr, vr, dvacc, dkacc, tail_bias);
         }
     };
     if (CAUSAL || k.key_tail)
         walk(std::true_type{});
     else
         walk(std::false_type{});
-    bwd_last_dq<D>(a, k, (k.nq - 1) * kBq, dSs, Kall);
+    bwd_last_dq<D, DET>(a, k, (k.nq - 1) * kBq, dSs, Kall);
 
     // dK (scaled) and dV rows of this wave's keys: register i -> key
     // n0w + acc_row(i, h32), lane -> d = DB*l32 + db.
@@ -560,6 +580,47 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     }
 }
 
+// Deterministic mode's second pass: dq[b, h, m, :] = the sum of the partial
+// slabs in ascending key order (slab j holds keys 128/NSPLIT * j onwards;
+// causal: only the slabs of the key blocks at or before row m, the ones the
+// main kernel wrote for it), one thread per 4 floats.  The order is fixed,
+// so dq is bitwise reproducible.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_reduce(BwdArgs a, int BH)
+{
+    constexpr int TPR = D / 4;
+    constexpr int NSPLIT = BwdLayout<D>::NSPLIT;
+    const int64_t slab = (int64_t)BH * a.S_pad * D;  // floats per slab
+    const int64_t n = (int64_t)BH * a.S * TPR;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
+         idx += (int64_t)gridDim.x * 256) {
+        const int sub = (int)(idx % TPR);
+        const int64_t row = idx / TPR;
+        const int bh = (int)(row / a.S);
+        const int m = (int)(row - (int64_t)bh * a.S);
+        const int nslab = (CAUSAL ? m / kBk + 1 : a.nkb) * NSPLIT;
+        const float *p = a.dq_part + ((int64_t)bh * a.S_pad + m) * D + 4 * sub;
+        f32x4 acc = *(const f32x4 *)p;
+        for (int j = 1; j < nslab; ++j) {
+            const f32x4 x = *(const f32x4 *)(p + j * slab);
+            acc[0] += x[0];
+            acc[1] += x[1];
+            acc[2] += x[2];
+            acc[3] += x[3];
+        }
+        const int b = bh / a.H;
+        const int hh = bh - b * a.H;
+        *(f32x4 *)(a.dq + (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub) = acc;
+    }
+}
+
+// Floats of the deterministic mode's dq partials: one (B*H, S_pad, D) slab
+// per 128 / NSPLIT keys, i.e. nkb * B*H * S_pad * 128 for every D.
+inline int64_t dq_part_floats(int64_t nkb, int64_t BH, int64_t S_pad)
+{
+    return nkb * BH * S_pad * (int64_t)kBk;
+}
+
 template <int D, bool CAUSAL>
 int launch_bwd(const BwdArgs &args, int64_t rows_pad, int nblocks)
 {
@@ -567,8 +628,18 @@ int launch_bwd(const BwdArgs &args, int64_t rows_pad, int nblocks)
     const int pre_blocks = (int)((rows_pad + RPB - 1) / RPB);
     hipLaunchKernelGGL((attn_bwd_pre<D>), dim3(pre_blocks), dim3(256), 0, 0, args, rows_pad);
     if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
-    hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
-    return launch_ok("attn_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+    if (!args.dq_part) {
+        hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL, false>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
+    hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL, true>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    if (!launch_ok("attn_bwd_kernel")) return EMBER_ERR_DEVICE;
+    const int BH = nblocks / args.nkb;
+    const int64_t n = (int64_t)BH * args.S * (D / 4);
+    const int64_t want = (n + 255) / 256;
+    const int grid = (int)(want < 16384 ? want : 16384);
+    hipLaunchKernelGGL((attn_bwd_dq_reduce<D, CAUSAL>), dim3(grid), dim3(256), 0, 0, args, BH);
+    return launch_ok("attn_bwd_dq_reduce") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 }  // namespace

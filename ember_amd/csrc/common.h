@@ -32,7 +32,11 @@ enum ScratchSlot {
     kScratchLayerNorm = 2,
     kScratchColSum = 3,
     kScratchGemmSplit = 4,
-    kScratchSlots = 5
+    kScratchAttnDqPart = 5,
+    kScratchSlots = 6
 };
+
+// The library-wide switch set by ember_set_deterministic.
+bool deterministic();
 
 }  // namespace ember

@@ -24,6 +24,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <unordered_map>
@@ -92,6 +93,33 @@ void *scratch(int slot, size_t bytes)
     s.ptr = p;
     s.bytes = want;
     return p;
+}
+
+// Frees every scratch buffer of `dev` (the current device), after the queued
+// work that may still read them has finished.
+void release_scratch(int dev)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    bool synced = false;
+    for (ScratchBuf &s : g_scratch[dev]) {
+        if (!s.ptr) continue;
+        if (!synced) {
+            hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize(empty_cache)");
+            synced = true;
+        }
+        hip_ok(hipFree(s.ptr), "hipFree(scratch)");
+        s.ptr = nullptr;
+        s.bytes = 0;
+    }
+}
+
+namespace {
+std::atomic<int> g_deterministic{0};
+}  // namespace
+
+bool deterministic()
+{
+    return g_deterministic.load(std::memory_order_relaxed) != 0;
 }
 
 namespace {
@@ -252,8 +280,22 @@ void ember_empty_cache(void)
 {
     int dev = 0;
     if (!ember::hip_ok(hipGetDevice(&dev), "hipGetDevice")) return;
-    std::lock_guard<std::mutex> lock(ember::g_alloc_mu);
-    if (dev >= 0 && dev < ember::kMaxDevices) ember::release_cached(dev);
+    if (dev < 0 || dev >= ember::kMaxDevices) return;
+    {
+        std::lock_guard<std::mutex> lock(ember::g_alloc_mu);
+        ember::release_cached(dev);
+    }
+    ember::release_scratch(dev);
+}
+
+void ember_set_deterministic(int enabled)
+{
+    ember::g_deterministic.store(enabled ? 1 : 0, std::memory_order_relaxed);
+}
+
+int ember_get_deterministic(void)
+{
+    return ember::deterministic() ? 1 : 0;
 }
 
 void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak)

@@ -56,10 +56,22 @@ void sync_device(void);
  * cache off.  No reference counterpart (memory_gpu.cu:10-28 calls
  * cudaMalloc/cudaFree each time); these two report and release the cache.
  * ember_empty_cache synchronises the current device and hipFrees every
- * cached block; ember_memory_stats gives the current device's bytes handed
+ * cached block and the library's own scratch buffers (attention_bwd's row
+ * statistics and dq partials, reduction partials), which are otherwise kept
+ * for reuse; ember_memory_stats gives the current device's bytes handed
  * out, bytes cached and peak bytes handed out (rounded block sizes). */
 void ember_empty_cache(void);
 void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak);
+
+/* Bitwise-reproducible results (no reference counterpart: the reference
+ * has no operator whose result depends on timing).  Off by default.  The
+ * only such operator here is attention_bwd's dq at S > 64 (see there); with
+ * the switch on it is formed in a fixed order instead, at the cost of a
+ * scratch buffer and one extra pass.  Every other operator of this library
+ * is reproducible either way.  The switch is process-wide; set it between
+ * calls, not while another thread is inside the library. */
+void ember_set_deterministic(int enabled);
+int ember_get_deterministic(void);
 
 /* ---- random tensors: replaces src/random/distributions.h:8-9 ----
  * (distributions_gpu.cu:11-32; called by src/random/random_api.c:70,88.)
@@ -147,11 +159,16 @@ int attention_fwd(const float *q, const float *k, const float *v, float *o, floa
  * 2*B*H*S_pad*4 bytes of device scratch (S_pad = S rounded up to 32; none at
  * S <= 64), which the library keeps cached between calls.
  * Determinism: dk and dv are bitwise reproducible.  For S > 64, dq is
- * accumulated in HBM with fp32 atomic adds from every key block that sees a
- * query row, so its last bits vary from run to run (each run within the
- * stated tolerance); at S <= 64 it is reproducible too.  Because of those
- * atomics dq must be device memory (not host or managed memory), and dq must
- * not overlap q, k, v, o, lse, d_o, dk or dv. */
+ * accumulated in HBM with fp32 atomic adds from every key block (128 keys)
+ * that sees a query row, so its last bits vary from run to run (each run
+ * within the stated tolerance); at S <= 64 it is reproducible too.  Because
+ * of those atomics dq must be device memory (not host or managed memory),
+ * and dq must not overlap q, k, v, o, lse, d_o, dk or dv.
+ * With ember_set_deterministic(1), S > 64 instead stores each key block's
+ * dq contribution in a scratch buffer of nkb*B*H*S_pad*D floats (nkb = S/128
+ * rounded up; 8 GiB at B4 H32 S4096 D128) and sums them per row in
+ * ascending key-block order in a second kernel: dq is then bitwise
+ * reproducible, and dk, dv are the same bits as without the switch. */
 int attention_bwd(const float *q, const float *k, const float *v, const float *o,
                   const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                   int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
@@ -171,7 +188,10 @@ int attention_bwd(const float *q, const float *k, const float *v, const float *o
  * are ordered because all library work runs on the null stream; launches of
  * this entry point that overlap on one GPU (for example replayed on several
  * streams at once) race on the array.  Each call writes every statistic it
- * reads before reading it, so nothing carries over between calls. */
+ * reads before reading it, so nothing carries over between calls.
+ * With ember_set_deterministic(1) and S > 64 it returns
+ * EMBER_ERR_UNSUPPORTED and launches nothing: the dq partials of that mode
+ * need a buffer of the problem's size. */
 int attention_bwd_noalloc(const float *q, const float *k, const float *v, const float *o,
                           const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                           int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,

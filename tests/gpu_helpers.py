@@ -22,6 +22,31 @@ def scale_for(D: int) -> float:
     return float(np.float32(1.0 / math.sqrt(D)))
 
 
+SENTINEL = np.float32(12345.0)
+
+
+def padded_strides(B, H, S, D, pad, hpad):
+    """Strides (sb, sh, ss) of a (B, H, S + hpad, D + pad) buffer, and its size."""
+    ss = D + pad
+    sh = (S + hpad) * ss
+    return (H * sh, sh, ss), B * H * sh
+
+
+def upload_padded(x, strides, total):
+    """x (B, H, S, D) into a padded device buffer whose padding is SENTINEL."""
+    buf = np.full(total, SENTINEL, np.float32)
+    view = np.lib.stride_tricks.as_strided(buf, shape=x.shape, strides=tuple(4 * s for s in strides) + (4,))
+    view[...] = x
+    return DeviceArray.from_numpy(buf)
+
+
+def download_padded(dev, strides, shape):
+    """The (B, H, S, D) view of a padded device buffer, and the whole buffer."""
+    buf = dev.numpy()
+    view = np.lib.stride_tricks.as_strided(buf, shape=shape, strides=tuple(4 * s for s in strides) + (4,))
+    return np.array(view), buf
+
+
 def attention_fwd(q, k, v, causal, scale=None):
     B, H, S, D = q.shape
     scale = scale_for(D) if scale is None else scale

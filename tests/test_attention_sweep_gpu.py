@@ -26,7 +26,8 @@ from ember_amd.capi import DeviceArray
 pytestmark = pytest.mark.gpu
 
 TOL = dict(rtol=1e-3, atol=2e-4)
-SENTINEL = np.float32(12345.0)
+SENTINEL = G.SENTINEL
+_strided, _download = G.padded_strides, G.download_padded
 
 
 def _case(seed):
@@ -68,28 +69,6 @@ def _wide_case(seed):
     return B, H, S, D, causal, pads, hpads
 
 
-def _strided(B, H, S, D, pad, hpad):
-    """Strides (sb, sh, ss) of a (B, H, S + hpad, D + pad) buffer."""
-    ss = D + pad
-    sh = (S + hpad) * ss
-    return (H * sh, sh, ss), B * H * sh
-
-
-def _upload(x, strides, total):
-    """x (B, H, S, D) into a padded device buffer; padding = SENTINEL."""
-    B, H, S, D = x.shape
-    buf = np.full(total, SENTINEL, np.float32)
-    view = np.lib.stride_tricks.as_strided(buf, shape=x.shape, strides=tuple(4 * s for s in strides) + (4,))
-    view[...] = x
-    return DeviceArray.from_numpy(buf), buf
-
-
-def _download(dev, strides, shape):
-    buf = dev.numpy()
-    view = np.lib.stride_tricks.as_strided(buf, shape=shape, strides=tuple(4 * s for s in strides) + (4,))
-    return np.array(view), buf
-
-
 @pytest.mark.parametrize("seed", range(64))
 def test_random_shape_and_layout(seed):
     _run(seed, *_case(seed))
@@ -127,9 +106,9 @@ def _run(seed, B, H, S, D, causal, pads, hpads):
     out_st, out_tot = _strided(B, H, S, D, pads[1], hpads[1])
     L = capi.lib()
     scale = G.scale_for(D)
-    dq_, dk_, dv_ = (_upload(x, in_st, in_tot)[0] for x in (q, k, v))
-    ddo = _upload(d_o, out_st, out_tot)[0]
-    o = _upload(np.zeros_like(q), out_st, out_tot)[0]
+    dq_, dk_, dv_ = (G.upload_padded(x, in_st, in_tot) for x in (q, k, v))
+    ddo = G.upload_padded(d_o, out_st, out_tot)
+    o = G.upload_padded(np.zeros_like(q), out_st, out_tot)
     lse = DeviceArray((B, H, S))
     capi.check(L.attention_fwd(dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr, B, H, S, D, scale, int(causal),
                                *in_st, *out_st), "attention_fwd")
@@ -140,7 +119,7 @@ def _run(seed, B, H, S, D, causal, pads, hpads):
     np.testing.assert_allclose(lse_np, lse_ref, **TOL)
     assert np.count_nonzero(o_buf == SENTINEL) == out_tot - B * H * S * D  # padding untouched
 
-    grads = [_upload(np.zeros_like(q), in_st, in_tot)[0] for _ in range(3)]
+    grads = [G.upload_padded(np.zeros_like(q), in_st, in_tot) for _ in range(3)]
     capi.check(L.attention_bwd(dq_.ptr, dk_.ptr, dv_.ptr, o.ptr, lse.ptr, ddo.ptr,
                                *(g.ptr for g in grads), B, H, S, D, scale, int(causal),
                                *in_st, *out_st), "attention_bwd")

@@ -78,6 +78,25 @@ def test_attention_rejects_bad_layouts():
     assert _fwd_call(S=0) == 0                         # empty: nothing to do
 
 
+def test_deterministic_switch_and_noalloc_refusal():
+    """ember_set_deterministic is host state (no device call); with it on,
+    attention_bwd_noalloc refuses S > 64 (its dq partials would need a
+    buffer) before any device work, and still accepts the empty problem."""
+    L = capi.lib()
+    assert capi.is_deterministic() is False
+    p = C.c_void_p(16)
+    st = (128 * 64, 128 * 64, 64)
+    try:
+        capi.set_deterministic(True)
+        assert L.ember_get_deterministic() == 1
+        assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 128, 64, 0.125, 1, *st, *st) == 2
+        assert L.ember_get_last_error() == 2
+        assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 0, 64, 0.125, 1, *st, *st) == 0
+    finally:
+        capi.set_deterministic(False)
+    assert L.ember_get_deterministic() == 0
+
+
 def test_capi_raises_on_sticky_error():
     _fwd_call(D=48)
     with pytest.raises(capi.EmberError):
