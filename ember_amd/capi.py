@@ -87,6 +87,10 @@ def lib() -> C.CDLL:
     L.ember_get_deterministic.restype = C.c_int
     L.adam_step.restype = C.c_int
     L.adam_step.argtypes = [C.POINTER(_vp)] * 4 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 4 + [_i64]
+    L.adamw_step.restype = C.c_int
+    L.adamw_step.argtypes = [C.POINTER(_vp)] * 4 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 5 + [_i64]
+    L.sgd_step.restype = C.c_int
+    L.sgd_step.argtypes = [C.POINTER(_vp)] * 3 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 2
     _lib = L
     return L
 
@@ -168,3 +172,20 @@ def adam_step(params, grads, means, variances, lr, beta1, beta2, eps, step) -> i
     sizes = (_i64 * n)(*(x.size for x in params))
     return lib().adam_step(table(params), table(grads), table(means), table(variances), sizes, n,
                            lr, beta1, beta2, eps, step)
+
+
+def adamw_step(params, grads, means, variances, lr, beta1, beta2, eps, weight_decay, step) -> int:
+    """adamw_step over lists of DeviceArray (same lengths and sizes)."""
+    n = len(params)
+    table = lambda xs: (_vp * n)(*(x.ptr for x in xs))  # noqa: E731
+    sizes = (_i64 * n)(*(x.size for x in params))
+    return lib().adamw_step(table(params), table(grads), table(means), table(variances), sizes, n,
+                            lr, beta1, beta2, eps, weight_decay, step)
+
+
+def sgd_step(params, grads, velocities, lr, momentum) -> int:
+    """sgd_step over lists of DeviceArray (same lengths and sizes)."""
+    n = len(params)
+    table = lambda xs: (_vp * n)(*(x.ptr for x in xs))  # noqa: E731
+    sizes = (_i64 * n)(*(x.size for x in params))
+    return lib().sgd_step(table(params), table(grads), table(velocities), sizes, n, lr, momentum)

@@ -963,28 +963,45 @@ static PyObject *py_attention_bwd_packed(PyObject *module, PyObject *args)
     return (PyObject *)g;
 }
 
-/* _adam_step(params, grads, means, variances, lr, beta1, beta2, eps, t):
- * lists of _Tensor of matching sizes; updates params, means, variances in
- * place with one fused launch per 48 tensors (replaces Adam.apply's 13
- * element-wise operators per parameter, ember/optim/adam.py:24-45). */
-static PyObject *py_adam_step(PyObject *module, PyObject *args)
+/* Fused optimiser steps over lists of _Tensor of matching sizes, updated in
+ * place with one launch per 48 tensors:
+ *   _adam_step(params, grads, means, variances, lr, beta1, beta2, eps, t)
+ *     replaces Adam.apply (ember/optim/adam.py:24-45);
+ *   _adamw_step(params, grads, means, variances, lr, beta1, beta2, eps,
+ *               weight_decay, t)  replaces AdamW.apply (adamw.py:33-56);
+ *   _sgd_step(params, grads, velocities, lr, momentum)  replaces SGD.apply
+ *     (sgd.py:25-35). */
+enum { OPT_ADAM, OPT_ADAMW, OPT_SGD };
+
+static PyObject *opt_step(PyObject *args, int rule, const char *name)
 {
-    PyObject *lists[4];
-    double lr, b1, b2, eps;
-    long long t;
-    (void)module;
-    if (!PyArg_ParseTuple(args, "O!O!O!O!ddddL", &PyList_Type, &lists[0], &PyList_Type, &lists[1],
-                          &PyList_Type, &lists[2], &PyList_Type, &lists[3], &lr, &b1, &b2, &eps, &t))
-        return NULL;
+    PyObject *lists[4] = {NULL, NULL, NULL, NULL};
+    double lr = 0, b1 = 0, b2 = 0, eps = 0, wd = 0, momentum = 0;
+    long long t = 1;
+    int nl = 4;
+    int ok;
+    if (rule == OPT_ADAM)
+        ok = PyArg_ParseTuple(args, "O!O!O!O!ddddL", &PyList_Type, &lists[0], &PyList_Type, &lists[1],
+                              &PyList_Type, &lists[2], &PyList_Type, &lists[3], &lr, &b1, &b2, &eps, &t);
+    else if (rule == OPT_ADAMW)
+        ok = PyArg_ParseTuple(args, "O!O!O!O!dddddL", &PyList_Type, &lists[0], &PyList_Type, &lists[1],
+                              &PyList_Type, &lists[2], &PyList_Type, &lists[3], &lr, &b1, &b2, &eps, &wd,
+                              &t);
+    else {
+        nl = 3;
+        ok = PyArg_ParseTuple(args, "O!O!O!dd", &PyList_Type, &lists[0], &PyList_Type, &lists[1],
+                              &PyList_Type, &lists[2], &lr, &momentum);
+    }
+    if (!ok) return NULL;
     const Py_ssize_t n = PyList_GET_SIZE(lists[0]);
-    for (int j = 1; j < 4; j++)
+    for (int j = 1; j < nl; j++)
         if (PyList_GET_SIZE(lists[j]) != n) {
             PyErr_Format(PyExc_ValueError, "Optimizer expected %zd gradients / states, got %zd", n,
                          PyList_GET_SIZE(lists[j]));
             return NULL;
         }
     if (n > INT_MAX) return PyErr_NoMemory();
-    float **tab = (float **)PyMem_Malloc((size_t)(4 * n + 1) * sizeof(float *));
+    float **tab = (float **)PyMem_Malloc((size_t)(nl * n + 1) * sizeof(float *));
     int64_t *sizes = (int64_t *)PyMem_Malloc((size_t)(n + 1) * sizeof(int64_t));
     if (!tab || !sizes) {
         PyMem_Free(tab);
@@ -992,10 +1009,10 @@ static PyObject *py_adam_step(PyObject *module, PyObject *args)
         return PyErr_NoMemory();
     }
     for (Py_ssize_t i = 0; i < n; i++) {
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < nl; j++) {
             PyObject *item = PyList_GET_ITEM(lists[j], i);
             if (!PyObject_TypeCheck(item, &TensorType)) {
-                PyErr_SetString(PyExc_TypeError, "_adam_step expects lists of _Tensor");
+                PyErr_Format(PyExc_TypeError, "%s expects lists of _Tensor", name);
                 goto fail;
             }
             tab[j * n + i] = ((TensorObject *)item)->d_ptr;
@@ -1007,17 +1024,42 @@ static PyObject *py_adam_step(PyObject *module, PyObject *args)
         sizes[i] = ((TensorObject *)PyList_GET_ITEM(lists[0], i))->size;
     }
     {
-        int st = adam_step(tab, (const float *const *)(tab + n), tab + 2 * n, tab + 3 * n, sizes,
-                           (int)n, lr, b1, b2, eps, (int64_t)t);
+        const float *const *g = (const float *const *)(tab + n);
+        int st;
+        if (rule == OPT_ADAM)
+            st = adam_step(tab, g, tab + 2 * n, tab + 3 * n, sizes, (int)n, lr, b1, b2, eps, (int64_t)t);
+        else if (rule == OPT_ADAMW)
+            st = adamw_step(tab, g, tab + 2 * n, tab + 3 * n, sizes, (int)n, lr, b1, b2, eps, wd,
+                            (int64_t)t);
+        else
+            st = sgd_step(tab, g, tab + 2 * n, sizes, (int)n, lr, momentum);
         PyMem_Free(tab);
         PyMem_Free(sizes);
-        if (raise_status(st, "_adam_step")) return NULL;
+        if (raise_status(st, name)) return NULL;
         Py_RETURN_NONE;
     }
 fail:
     PyMem_Free(tab);
     PyMem_Free(sizes);
     return NULL;
+}
+
+static PyObject *py_adam_step(PyObject *module, PyObject *args)
+{
+    (void)module;
+    return opt_step(args, OPT_ADAM, "_adam_step");
+}
+
+static PyObject *py_adamw_step(PyObject *module, PyObject *args)
+{
+    (void)module;
+    return opt_step(args, OPT_ADAMW, "_adamw_step");
+}
+
+static PyObject *py_sgd_step(PyObject *module, PyObject *args)
+{
+    (void)module;
+    return opt_step(args, OPT_SGD, "_sgd_step");
 }
 
 static PyObject *py_synchronize(PyObject *module, PyObject *unused)
@@ -1071,6 +1113,8 @@ static PyMethodDef module_methods[] = {
     METHOD("_attention_fwd", py_attention_fwd, "fused attention forward -> (o, lse)"),
     METHOD("_attention_bwd", py_attention_bwd, "fused attention backward -> (dq, dk, dv)"),
     METHOD("_adam_step", py_adam_step, "fused Adam step over lists of _Tensor, in place"),
+    METHOD("_adamw_step", py_adamw_step, "fused AdamW step over lists of _Tensor, in place"),
+    METHOD("_sgd_step", py_sgd_step, "fused SGD (momentum) step over lists of _Tensor, in place"),
     METHOD("_linear", py_linear, "act(x @ w + bias) + residual -> (y, pre)"),
     METHOD("_gemm", py_gemm, "op(a) @ op(b) + bias + residual with either operand transposed in place"),
     METHOD("_gelu_bwd", py_gelu_bwd, "backward of Ember's GELU"),

@@ -207,10 +207,13 @@ class Linear(Layer):
         return input_grad(grad_y, self.w)
 
 
-class GELU(Layer):
-    """Ember's GELU, 0.5*x*(1 + tanh(0.8x)) (``ember/nn/activations.py:51-66``):
-    the forward composed from element-wise operators as the reference does,
-    the backward one fused kernel."""
+class Activation(Layer):
+    """A parameter-free element-wise layer (``ember/nn/base.py:38-47``); its
+    ``forward`` keeps x and y for ``backward``, so it may be called directly
+    as well as through ``__call__``."""
+
+    def __init__(self) -> None:
+        self.reset()
 
     def reset(self) -> None:
         self.x = self.y = None
@@ -221,9 +224,101 @@ class GELU(Layer):
     def gradients(self) -> list[Tensor | None]:
         return []
 
+    def _need_forward(self) -> None:
+        if self.y is None:
+            raise RuntimeError("forward() must run before backward()")
+
+
+class ReLU(Activation):
+    """max(x, 0); backward grad * (y > 0) (``ember/nn/activations.py:7-19``)."""
+
+    def forward(self, x: Tensor, training: bool = True) -> Tensor:
+        from ember_amd.tensor import max as em_max
+        self.x = x
+        self.y = em_max(x, 0)
+        return self.y
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        self._need_forward()
+        return grad_y * (self.y > 0.0)
+
+
+class Sigmoid(Activation):
+    """1 / (1 + exp(-x)); backward grad * (y * (1 - y))
+    (``ember/nn/activations.py:22-34``)."""
+
+    def forward(self, x: Tensor, training: bool = True) -> Tensor:
+        from ember_amd.tensor import exp
+        self.x = x
+        self.y = 1.0 / (1.0 + exp(-x))
+        return self.y
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        self._need_forward()
+        return grad_y * (self.y * (1.0 - self.y))
+
+
+class Tanh(Activation):
+    """tanh(x); backward grad * (1 - y*y) (``ember/nn/activations.py:37-49``)."""
+
     def forward(self, x: Tensor, training: bool = True) -> Tensor:
         from ember_amd.tensor import tanh
-        return 0.5 * x * (1 + tanh(0.8 * x))
+        self.x = x
+        self.y = tanh(x)
+        return self.y
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        self._need_forward()
+        return grad_y * (1 - self.y * self.y)
+
+
+class Dropout(Layer):
+    """Inverted dropout (``ember/nn/layers.py:59-97``): in training, keep
+    each element where a uniform(0, 1) draw exceeds p and scale the kept ones
+    by 1/(1-p); identity otherwise.  The mask comes from the library's
+    seeded generator (``ember_amd.random``)."""
+
+    def __init__(self, p: float):
+        if not 0 <= p < 1:
+            raise ValueError("p must be between 0 and 1 (exclusive of 1)")
+        self.p = p
+        self.scale = 1.0 / (1.0 - p)
+        self.reset()
+
+    def reset(self) -> None:
+        self.x = self.y = self.mask = None
+
+    def parameters(self) -> list[Tensor]:
+        return []
+
+    def gradients(self) -> list[Tensor | None]:
+        return []
+
+    def forward(self, x: Tensor, training: bool = True) -> Tensor:
+        self.x = x
+        if training:
+            self.mask = _random.uniform(0.0, 1.0, x.shape) > self.p
+            self.y = x * self.mask * self.scale
+        else:
+            self.y = x
+        return self.y
+
+    def backward(self, grad_y: Tensor) -> Tensor:
+        if self.mask is None:
+            raise RuntimeError("forward(training=True) must run before backward()")
+        return grad_y * self.mask * self.scale
+
+
+class GELU(Activation):
+    """Ember's GELU, 0.5*x*(1 + tanh(0.8x)) (``ember/nn/activations.py:51-66``):
+    the forward composed from element-wise operators as the reference does,
+    the backward one fused kernel."""
+
+    def forward(self, x: Tensor, training: bool = True) -> Tensor:
+        from ember_amd.tensor import tanh
+        self.x = x
+        self.y = 0.5 * x * (1 + tanh(0.8 * x))
+        return self.y
 
     def backward(self, grad_y: Tensor) -> Tensor:
         if self.x is None or self.y is None:

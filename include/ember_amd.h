@@ -215,6 +215,24 @@ int adam_step(float *const *params, const float *const *grads, float *const *exp
               float *const *exp_avg_sq, const int64_t *sizes, int ntensors, double lr,
               double beta1, double beta2, double eps, int64_t step);
 
+/* ---- fused AdamW: replaces ember/optim/adamw.py:33-56 (AdamW.apply) ----
+ * adam_step's m, v, m_hat, v_hat, then the decoupled decay and the Adam
+ * step, each an fp32 operation in Ember's order:
+ *   p = p - p*(lr*wd);  p = p - ((m/(1-b1^t))*lr) / (sqrt(v/(1-b2^t)) + eps)
+ * with lr*wd one double product rounded to fp32 (Python forms it before the
+ * tensor multiply), so the result is bit-identical to the reference's
+ * composed operators.  Same arguments and errors as adam_step plus
+ * weight_decay. */
+int adamw_step(float *const *params, const float *const *grads, float *const *exp_avg,
+               float *const *exp_avg_sq, const int64_t *sizes, int ntensors, double lr,
+               double beta1, double beta2, double eps, double weight_decay, int64_t step);
+
+/* ---- fused SGD: replaces ember/optim/sgd.py:25-35 (SGD.apply) ----
+ * v = v*momentum;  v = v + g;  p = p - v*lr  (fp32, Ember's order; v is the
+ * velocity, updated in place), over `ntensors` tensors as adam_step. */
+int sgd_step(float *const *params, const float *const *grads, float *const *velocity,
+             const int64_t *sizes, int ntensors, double lr, double momentum);
+
 /* ---- transformer-block pieces (config 5's pre-LN decoder block) ----
  * None has a counterpart in the reference; each replaces a composition of
  * its element-wise operators.  All return a status and launch nothing on an

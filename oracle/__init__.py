@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
         L.oracle_attention_bwd.argtypes = [_f32p] * 9 + [_i64] * 4 + [C.c_float, C.c_int] + [_i64] * 6
         L.oracle_attention_bwd.restype = C.c_int
         L.oracle_adam_step.argtypes = [_f32p] * 4 + [_i64] + [C.c_double] * 4 + [_i64]
+        L.oracle_adamw_step.argtypes = [_f32p] * 4 + [_i64] + [C.c_double] * 5 + [_i64]
+        L.oracle_sgd_step.argtypes = [_f32p] * 3 + [_i64] + [C.c_double] * 2
         L.oracle_layernorm_fwd.argtypes = [_f32p] * 6 + [_i64, _i64, C.c_float]
         L.oracle_layernorm_bwd.argtypes = [_f32p] * 8 + [_i64, _i64]
         L.oracle_gelu_fwd.argtypes = [_f32p, _f32p, _i64]
@@ -340,6 +342,76 @@ def ref_composed_adam_step(p, g, m, v, lr, beta1, beta2, eps, t):
     den = scal("add_scalar", sq, eps)                                     # sqrt(v_hat) + eps
     p = ten("sub_tensor", p, ten("truediv_tensor", num, den))             # p -= num / den
     return p, m, v
+
+
+def adamw_step(p, g, m, v, lr, beta1, beta2, eps, weight_decay, t):
+    """In-place AdamW step, as Ember's AdamW.apply computes it
+    (ember/optim/adamw.py:33-56)."""
+    for x in (p, g, m, v):
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().oracle_adamw_step(p, g, m, v, p.size, lr, beta1, beta2, eps, weight_decay, t)
+
+
+def sgd_step(p, g, v, lr, momentum):
+    """In-place SGD (momentum) step, as Ember's SGD.apply computes it
+    (ember/optim/sgd.py:25-35)."""
+    for x in (p, g, v):
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+    lib().oracle_sgd_step(p, g, v, p.size, lr, momentum)
+
+
+def _ref_ops(n):
+    """(scal, ten, sqrt) runners of the reference's own CPU operators on
+    float32 vectors of n elements; scalars rounded to float32 as the
+    binding's "f" conversion does."""
+    R = ref_lib()
+    f32 = np.float32
+
+    def scal(fn, a, x):
+        out = np.empty(n, dtype=np.float32)
+        getattr(R, fn)(a, f32(x), out, n)
+        return out
+
+    def ten(fn, a, b):
+        out = np.empty(n, dtype=np.float32)
+        getattr(R, fn)(a, b, out, n)
+        return out
+
+    def sqrt(a):
+        out = np.empty(n, dtype=np.float32)
+        R.sqrt_tensor(a, out, n)
+        return out
+
+    return scal, ten, sqrt
+
+
+def ref_composed_adamw_step(p, g, m, v, lr, beta1, beta2, eps, weight_decay, t):
+    """(p, m, v) after one AdamW step run through the reference's CPU
+    operators in adamw.py's order (:45-56)."""
+    p, g, m, v = (np.ascontiguousarray(x, dtype=np.float32).reshape(-1) for x in (p, g, m, v))
+    scal, ten, sqrt = _ref_ops(p.size)
+    m = scal("mul_scalar", m, beta1)
+    m = ten("add_tensor", m, scal("mul_scalar", g, 1 - beta1))
+    v = scal("mul_scalar", v, beta2)
+    v = ten("add_tensor", v, scal("mul_scalar", ten("mul_tensor", g, g), 1 - beta2))
+    m_hat = scal("truediv_scalar", m, 1 - beta1 ** t)
+    v_hat = scal("truediv_scalar", v, 1 - beta2 ** t)
+    p = ten("sub_tensor", p, scal("mul_scalar", p, lr * weight_decay))   # p -= lr*wd*p
+    num = scal("mul_scalar", m_hat, lr)
+    den = scal("add_scalar", sqrt(v_hat), eps)
+    p = ten("sub_tensor", p, ten("truediv_tensor", num, den))
+    return p, m, v
+
+
+def ref_composed_sgd_step(p, g, v, lr, momentum):
+    """(p, v) after one SGD step run through the reference's CPU operators in
+    sgd.py's order (:33-35)."""
+    p, g, v = (np.ascontiguousarray(x, dtype=np.float32).reshape(-1) for x in (p, g, v))
+    scal, ten, _ = _ref_ops(p.size)
+    v = scal("mul_scalar", v, momentum)
+    v = ten("add_tensor", v, g)
+    p = ten("sub_tensor", p, scal("mul_scalar", v, lr))
+    return p, v
 
 
 # --------------------------------------------- LayerNorm, GELU (block pieces)

@@ -227,6 +227,51 @@ void oracle_adam_step(float *p, const float *g, float *m, float *v, int64_t n, d
     }
 }
 
+/* ---- AdamW: restates ember/optim/adamw.py:33-56 as Ember executes it ----
+ * adam.py's m, v, m_hat, v_hat (adamw.py:45-52), then
+ *   p -= lr * weight_decay * p      (:55; Python forms lr*wd in double first)
+ *   p -= lr * m_hat / (sqrt(v_hat) + eps)                             (:56)
+ * each an fp32 operator of the reference, scalars rounded to float once. */
+void oracle_adamw_step(float *p, const float *g, float *m, float *v, int64_t n, double lr,
+                       double beta1, double beta2, double eps, double weight_decay, int64_t t)
+{
+    const float b1 = (float)beta1, omb1 = (float)(1.0 - beta1);
+    const float b2 = (float)beta2, omb2 = (float)(1.0 - beta2);
+    const float bc1 = (float)(1.0 - pow(beta1, (double)t));
+    const float bc2 = (float)(1.0 - pow(beta2, (double)t));
+    const float flr = (float)lr, feps = (float)eps, lrwd = (float)(lr * weight_decay);
+    for (int64_t i = 0; i < n; i++) {
+        float mi = m[i] * b1;
+        const float gm = g[i] * omb1;
+        mi = mi + gm;
+        float vi = v[i] * b2;
+        const float gg = g[i] * g[i];
+        const float gv = gg * omb2;
+        vi = vi + gv;
+        const float mh = mi / bc1;
+        const float vhat = vi / bc2;
+        const float decay = p[i] * lrwd;      /* (lr * wd) * p                   */
+        const float pd = p[i] - decay;        /* p -= ...                        */
+        const float num = mh * flr;
+        const float den = sqrtf(vhat) + feps;
+        p[i] = pd - num / den;
+        m[i] = mi;
+        v[i] = vi;
+    }
+}
+
+/* ---- SGD: restates ember/optim/sgd.py:25-35 as Ember executes it ----
+ *   v *= momentum;  v += g;  p -= lr * v     (sgd.py:33-35), fp32 each. */
+void oracle_sgd_step(float *p, const float *g, float *v, int64_t n, double lr, double momentum)
+{
+    const float flr = (float)lr, fmom = (float)momentum;
+    for (int64_t i = 0; i < n; i++) {
+        const float vi = v[i] * fmom + g[i];  /* two roundings: contraction off */
+        p[i] = p[i] - vi * flr;
+        v[i] = vi;
+    }
+}
+
 /* ---- LayerNorm (build-defined; Ember has none) ----
  * mean, var (biased) and the backward's row means in FP64, outputs cast to
  * float once, Ember style.  Row-major (rows x d). */

@@ -275,6 +275,106 @@ def test_oracle_adam_planted_mistakes_fail():
     assert not np.allclose(bad[0], good[0], rtol=1e-6)
 
 
+# ------------------------------------------------------------ AdamW, SGD
+
+
+@needs_ref
+@pytest.mark.parametrize("hp", [(1e-3, 0.9, 0.999, 1e-8, 0.01), (0.01, 0.8, 0.99, 1e-6, 0.1),
+                                (0.1, 0.5, 0.9, 1e-3, 0.5), (0.01, 0.9, 0.999, 1e-8, 0.0)])
+@pytest.mark.parametrize("t", [1, 2, 17])
+def test_oracle_adamw_is_bitwise_the_reference_composition(hp, t):
+    """oracle_adamw_step == adamw.py's element-wise ops (:45-56) run through
+    the reference's own compiled operators_cpu.c, bit for bit."""
+    lr, b1, b2, eps, wd = hp
+    p, g, m, v = _adam_state(1000, t)
+    rp, rm, rv = oracle.ref_composed_adamw_step(p, g, m, v, lr, b1, b2, eps, wd, t)
+    oracle.adamw_step(p, g, m, v, lr, b1, b2, eps, wd, t)
+    assert np.array_equal(p, rp) and np.array_equal(m, rm) and np.array_equal(v, rv)
+
+
+def test_oracle_adamw_special_cases():
+    """weight_decay = 0 is Adam bit for bit (p - p*0 == p); with g = m = v = 0
+    the Adam term is exactly 0 and p becomes p - p*fp32(lr*wd), the
+    reference's test_weight_decay_shrinks_params_without_grad in closed form."""
+    lr, b1, b2, eps = 0.01, 0.9, 0.999, 1e-8
+    base = _adam_state(300, 5)
+    a, w = [x.copy() for x in base], [x.copy() for x in base]
+    oracle.adam_step(*a, lr, b1, b2, eps, 3)
+    oracle.adamw_step(*w, lr, b1, b2, eps, 0.0, 3)
+    assert all(np.array_equal(x, y) for x, y in zip(a, w))
+    p = base[0].copy()
+    z = np.zeros_like(p)
+    m, v = z.copy(), z.copy()
+    oracle.adamw_step(p, z.copy(), m, v, 0.1, b1, b2, eps, 0.5, 1)
+    p0 = base[0]
+    assert np.array_equal(p, p0 - p0 * np.float32(0.1 * 0.5))
+    assert np.all(np.abs(p) < np.abs(p0) + (p0 == 0))
+
+
+def test_oracle_adamw_matches_the_textbook_formula():
+    """The reference's own test formula (tests/optim/test_adamw.py:9-17),
+    float64, three steps."""
+    lr, b1, b2, eps, wd = 0.01, 0.9, 0.999, 1e-8, 0.1
+    p, g, m, v = _adam_state(500, 6)
+    P, G, M, V = (x.astype(np.float64) for x in (p, g, m, v))
+    for t in (1, 2, 3):
+        M = b1 * M + (1 - b1) * G
+        V = b2 * V + (1 - b2) * G * G
+        P = P - lr * wd * P
+        P = P - lr * (M / (1 - b1 ** t)) / (np.sqrt(V / (1 - b2 ** t)) + eps)
+        oracle.adamw_step(p, g, m, v, lr, b1, b2, eps, wd, t)
+    np.testing.assert_allclose(p, P, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(m, M, rtol=1e-5, atol=1e-7)
+
+
+@needs_ref
+def test_oracle_adamw_planted_mistakes_fail():
+    """Decay applied after the Adam step instead of before, or dropped, must
+    not pass the bitwise comparison with the reference's composition."""
+    lr, b1, b2, eps, wd = 0.1, 0.9, 0.999, 1e-8, 0.5
+    base = _adam_state(400, 7)
+    rp, _, _ = oracle.ref_composed_adamw_step(*base, lr, b1, b2, eps, wd, 1)
+    adam = [x.copy() for x in base]
+    oracle.adam_step(*adam, lr, b1, b2, eps, 1)                  # no decay
+    assert not np.array_equal(adam[0], rp)
+    late = adam[0] - adam[0] * np.float32(lr * wd)                # decay after the step
+    assert not np.array_equal(late, rp)
+
+
+@needs_ref
+@pytest.mark.parametrize("lr,momentum", [(0.1, 0.0), (0.01, 0.9), (0.5, 0.99)])
+def test_oracle_sgd_is_bitwise_the_reference_composition(lr, momentum):
+    """oracle_sgd_step == sgd.py:33-35 run through the reference's compiled
+    operators, over three steps."""
+    p, g, _, v = _adam_state(1000, 8)
+    rp, rv = p.copy(), v.copy()
+    for _ in range(3):
+        rp, rv = oracle.ref_composed_sgd_step(rp, g, rv, lr, momentum)
+        oracle.sgd_step(p, g, v, lr, momentum)
+        assert np.array_equal(p, rp) and np.array_equal(v, rv)
+
+
+def test_oracle_sgd_closed_forms_and_planted_mistake():
+    """momentum 0: p - g*lr exactly and v = g; the reference's test formula
+    (tests/optim/test_sgd.py:9-12) in float64; swapping lr and momentum fails."""
+    p, g, _, _ = _adam_state(400, 9)
+    v = np.zeros_like(p)
+    q = p.copy()
+    oracle.sgd_step(q, g, v, 0.1, 0.0)
+    assert np.array_equal(q, p - g * np.float32(0.1)) and np.array_equal(v, g)
+    P, V = p.astype(np.float64), np.zeros(p.size)
+    q, v = p.copy(), np.zeros_like(p)
+    for _ in range(3):
+        V = 0.9 * V + g
+        P = P - 0.05 * V
+        oracle.sgd_step(q, g, v, 0.05, 0.9)
+    np.testing.assert_allclose(q, P, rtol=1e-5, atol=1e-6)
+    bad, bv = p.copy(), np.zeros_like(p)
+    for _ in range(3):
+        oracle.sgd_step(bad, g, bv, 0.9, 0.05)
+    assert not np.allclose(bad, P, rtol=1e-3)
+
+
 # ------------------------------------------------------ LayerNorm and GELU
 
 
