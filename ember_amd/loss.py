@@ -3,12 +3,28 @@
 from __future__ import annotations
 
 import math
+from abc import ABC, abstractmethod
 
 from ember_amd import _core as C
 from ember_amd.tensor import Tensor, amax, exp, log, sum as _sum
 
 
-class MSELoss:
+class Loss(ABC):
+    """Base class (``ember/loss/base.py:6-22``): ``forward`` returns the scalar
+    loss and keeps what ``backward`` needs; ``backward`` returns the gradient
+    with respect to ``pred``."""
+
+    def __call__(self, pred: Tensor, target: Tensor) -> float:
+        return self.forward(pred, target)
+
+    @abstractmethod
+    def forward(self, pred: Tensor, target: Tensor) -> float: ...
+
+    @abstractmethod
+    def backward(self) -> Tensor: ...
+
+
+class MSELoss(Loss):
     """Mean squared error over all elements (``losses.py:9-26``):
     forward returns mean((pred - target)^2), backward (2/n)*(pred - target).
 
@@ -31,9 +47,6 @@ class MSELoss:
         self.diff = pred - target
         return _sum(self.diff * self.diff) / self.n
 
-    def __call__(self, pred: Tensor, target: Tensor) -> float:
-        return self.forward(pred, target)
-
     def backward(self) -> Tensor:
         if self.grad is not None:
             return self.grad
@@ -42,7 +55,7 @@ class MSELoss:
         return (2.0 / self.n) * self.diff
 
 
-class CrossEntropyLoss:
+class CrossEntropyLoss(Loss):
     """Softmax cross-entropy over (batch, classes) logits against one-hot (or
     probability) targets, averaged over the batch (``losses.py:29-56``):
     forward -sum(target * log_softmax(pred)) / batch with the log-sum-exp
@@ -61,13 +74,10 @@ class CrossEntropyLoss:
         self.probs = exp(log_probs)
         return -_sum(target * log_probs) / self.n
 
-    def __call__(self, pred: Tensor, target: Tensor) -> float:
-        return self.forward(pred, target)
-
     def backward(self) -> Tensor:
         if self.probs is None or self.target is None:
             raise RuntimeError("forward() must run before backward()")
         return (self.probs - self.target) / self.n
 
 
-__all__ = ["MSELoss", "CrossEntropyLoss"]
+__all__ = ["Loss", "MSELoss", "CrossEntropyLoss"]

@@ -172,3 +172,58 @@ def test_type_stubs_match_the_binding_modules(module):
         cls = next(n for n in tree.body if isinstance(n, ast.ClassDef) and n.name == "_Tensor")
         members = {n.name for n in cls.body if isinstance(n, ast.FunctionDef)} - {"__init__"}
         assert members <= set(dir(mod._Tensor)), sorted(members - set(dir(mod._Tensor)))
+
+
+def _reference_classes(relpath):
+    """{class name: (base names, {method: {arg: default}})} of a reference
+    source file, read as text (nothing of it is imported or run)."""
+    import ast
+    import os
+
+    tree = ast.parse(open(os.path.join("/root/reference", relpath)).read())
+    out = {}
+    for node in tree.body:
+        if not isinstance(node, ast.ClassDef):
+            continue
+        methods = {}
+        for f in node.body:
+            if isinstance(f, ast.FunctionDef):
+                args = f.args.args[len(f.args.args) - len(f.args.defaults):]
+                methods[f.name] = {a.arg: ast.literal_eval(d) for a, d in zip(args, f.args.defaults)}
+        out[node.name] = ([b.id for b in node.bases if isinstance(b, ast.Name)], methods)
+    return out
+
+
+@pytest.mark.skipif(not __import__("os").path.isdir("/root/reference/ember"),
+                    reason="needs the reference checkout (read as text)")
+@pytest.mark.parametrize("relpath,module", [
+    ("ember/nn/activations.py", "nn"), ("ember/nn/layers.py", "nn"), ("ember/nn/base.py", "nn"),
+    ("ember/optim/adam.py", "optim"), ("ember/optim/adamw.py", "optim"), ("ember/optim/sgd.py", "optim"),
+    ("ember/loss/base.py", "loss"), ("ember/loss/losses.py", "loss"),
+])
+def test_nn_optim_loss_classes_mirror_the_reference(relpath, module):
+    """Every class of the reference's nn / optim / loss modules exists here
+    with the same base class, the same public methods and the same
+    constructor defaults (no device work: nothing is instantiated)."""
+    import inspect
+
+    mod = getattr(em, module)
+    for name, (bases, methods) in _reference_classes(relpath).items():
+        cls = getattr(mod, name, None)
+        assert cls is not None, f"{module}.{name} missing"
+        for b in bases:
+            if b != "ABC":
+                assert issubclass(cls, getattr(mod, b)), (name, b)
+        for meth, defaults in methods.items():
+            if meth.startswith("_") and meth not in ("__init__", "__call__"):
+                continue
+            assert hasattr(cls, meth), f"{module}.{name}.{meth}"
+            params = inspect.signature(getattr(cls, meth)).parameters
+            for arg, value in defaults.items():
+                assert arg in params and params[arg].default == value, (name, meth, arg)
+
+
+def test_dropout_rejects_bad_probability():
+    for p in (1.0, -0.1, 1.5):
+        with pytest.raises(ValueError):
+            em.nn.Dropout(p)
