@@ -272,10 +272,10 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
                                   "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
         del q, k, v, o, lse
     # The backward in the same regime: algorithmic bytes 32*B*H*S*D + 8*B*H*S
-    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 32: one wave per head
-    # (D = 64) or one LDS-staged workgroup per head (D = 128); S = 64: one wave
-    # per key block (D = 64) or the workgroup kernel (D = 128); S = 128: the
-    # workgroup kernel.
+    # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 64: LDS-staged
+    # workgroups (one per head at S <= 32, persistent with a register
+    # prefetch of the next head at S = 64); S = 128: the key-block workgroup
+    # kernel.
     for S, D in ((32, 64), (32, 128), (64, 64), (64, 128), (128, 64), (128, 128)):
         B, H = (1 << 20) // S // 64, 64
         n = B * H * S * D

@@ -14,12 +14,35 @@
 // D = 128, while for non-causal D = 128 the default allocation cycles the
 // 128 dK/dV accumulators between AGPRs and VGPRs every query block and runs
 // 2x slower than the VGPR form (and D = 64 causal is 6 % faster in VGPR form).
+#include <atomic>
 #include <mutex>
 
 #include "attention_bwd_kernels.h"
 
 namespace ember {
 namespace {
+
+// Compute units of the current device (cached per device): the grid of the
+// persistent kernels below.
+int device_cus(int *out)
+{
+    constexpr int kDevices = 16;
+    static std::atomic<int> cached[kDevices];
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return EMBER_ERR_DEVICE;
+    if (dev >= 0 && dev < kDevices && cached[dev].load() > 0) {
+        *out = cached[dev].load();
+        return EMBER_OK;
+    }
+    int n = 0;
+    if (!hip_ok(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+                "hipDeviceGetAttribute"))
+        return EMBER_ERR_DEVICE;
+    n = n > 0 ? n : 1;
+    if (dev >= 0 && dev < kDevices) cached[dev].store(n);
+    *out = n;
+    return EMBER_OK;
+}
 
 // Short sequences at D = 128 (S <= 32): one workgroup of 4 waves per head,
 // the head's Q, K, V and dO staged in LDS by direct HBM -> LDS copies
@@ -185,8 +208,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_short_lds(BwdArgs a)
     }
 }
 
-// 32 < S <= 64 at D = 128: the same scheme with 64-row tiles, one
-// workgroup of 8 waves per head (one per CU: Q, K, dO and V take 132 KB).
+// 32 < S <= 64 at D = 128: the same scheme with 64-row tiles and a
+// workgroup of 8 waves (Q, K, dO and V take 132 KB of LDS: one per CU).
 // P^T and dS^T (64 x 68 floats each) overlay the V tile once every wave is
 // past its dP products, so P and dS wait in registers across one barrier.
 //   wave w: S / dP quadrants w and w + 8 of the 4 x 4 grid of 16 x 16
@@ -206,8 +229,22 @@ struct ShortLds64 {
     static constexpr int VP = TILE > 2 * R * PSTR ? TILE : 2 * R * PSTR;
 };
 
+// The kernel is persistent: one workgroup per CU walks heads blockIdx.x,
+// blockIdx.x + gridDim.x, ...  The tiles take the whole LDS, so no second
+// workgroup can overlap one head's HBM traffic with another's products;
+// instead each thread prefetches its row share of the next head (Q, K, V,
+// dO and O: 8 lanes per row, 16 floats of each) into registers while the
+// current head is multiplied (+13-23 % against one workgroup per head,
+// which loaded, then multiplied).  Per iteration:
+//   barrier (the previous head's products are done with LDS);
+//   prefetched rows -> LDS tiles, delta and lse2 from them;
+//   prefetch the next head's rows; barrier;
+//   S / dP of the quadrants, P / dS, then dV / dK / dQ; store them.
+// Vector-memory operations retire in issue order and the stores are the
+// last ones of an iteration, so the wait for the prefetched rows at the
+// next iteration's top is vmcnt(stores): it does not wait for the stores.
 template <bool CAUSAL>
-__global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64(BwdArgs a)
+__global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int nbh)
 {
     typedef ShortLds64 L;
     constexpr int D = L::D, R = L::R;
@@ -222,155 +259,168 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64(BwdArgs a)
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int bh = blockIdx.x;
-    const int b = bh / a.H;
-    const int hh = bh - b * a.H;
     const int S = a.S;
     const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
-    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
-    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
-
-    {
-        const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
-        const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
-        const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
-        const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
-#pragma unroll
-        for (int t = w; t < L::COP; t += L::NW) {
-            const int p = 64 * t + lane;
-            int r = p / L::ROWCH;
-            const int c = p - r * L::ROWCH;
-            const bool real = r < R && c < D / 4;
-            r = r < S ? r : S - 1;
-            const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
-            const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
-            dma16_buf(rq, oi, Qs + 256 * t);
-            dma16_buf(rk, oi, Ks + 256 * t);
-            dma16_buf(rv, oi, Vs + 256 * t);
-            dma16_buf(rg, og, Gs + 256 * t);
-        }
-    }
-    {
-        const int j = 8 * w + (lane >> 3);
-        const int s8 = lane & 7;
-        const int jr = j < S ? j : S - 1;
-        const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
-        const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
-        float part = 0.0f;
+    // Staging and row statistics: row j, 8 lanes per row, columns 32 it + 4 s8.
+    const int j = 8 * w + (lane >> 3), s8 = lane & 7;
+    const int jr = j < S ? j : S - 1;  // rows past S re-read row S-1 (masked later)
+    auto in_base_of = [&](int bh) {
+        const int b = bh / a.H;
+        return (int64_t)b * a.in_sb + (int64_t)(bh - b * a.H) * a.in_sh;
+    };
+    auto out_base_of = [&](int bh) {
+        const int b = bh / a.H;
+        return (int64_t)b * a.out_sb + (int64_t)(bh - b * a.H) * a.out_sh;
+    };
+    f32x4 rq[D / 32], rk[D / 32], rv[D / 32], rg[D / 32], ro[D / 32];
+    float lse_v = 0.0f;
+    auto prefetch = [&](int bh) {
+        const int64_t ib = in_base_of(bh) + (int64_t)jr * in_ss + 4 * s8;
+        const int64_t ob = out_base_of(bh) + (int64_t)jr * out_ss + 4 * s8;
 #pragma unroll
         for (int it = 0; it < D / 32; ++it) {
-            const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
-            const f32x4 g4 = *(const f32x4 *)(grow + 32 * it + 4 * s8);
-            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
+            rq[it] = *(const f32x4 *)(a.q + ib + 32 * it);
+            rk[it] = *(const f32x4 *)(a.k + ib + 32 * it);
+            rv[it] = *(const f32x4 *)(a.v + ib + 32 * it);
+            rg[it] = *(const f32x4 *)(a.dout + ob + 32 * it);
+            ro[it] = *(const f32x4 *)(a.o + ob + 32 * it);
         }
-        part += __shfl_xor(part, 1);
-        part += __shfl_xor(part, 2);
-        part += __shfl_xor(part, 4);
-        if (s8 == 0) {
-            L2s[j] = j < S ? a.lse[(int64_t)bh * S + j] * kLog2e : INFINITY;
-            DLs[j] = j < S ? part : 0.0f;
-        }
-    }
-    wait_vmem();
-    __syncthreads();
+        lse_v = a.lse[(int64_t)bh * S + jr];
+    };
 
-    // ---- S, dP, P, dS of quadrants w and w + 8 ----
-    const int l16 = lane & 15, g4 = lane >> 4;
-    float pv[2][4], dv4[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int quad = w + 8 * u;
-        const int qm = quad >> 2, qn = quad & 3;
-        const int key = 16 * qn + l16;
-        f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
-        if (!CAUSAL || qn <= qm) {
-            const int arow = (16 * qm + l16) * L::STR + 4 * g4;
-            const int brow = key * L::STR + 4 * g4;
-#pragma unroll
-            for (int c0 = 0; c0 < D; c0 += 16) {
-                const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
-                const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
-                const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
-                const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[j], kf[j], sacc, 0, 0, 0);
-                    pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[j], vf[j], pacc, 0, 0, 0);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int qi = 16 * qm + 4 * g4 + r;
-            float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
-            const bool vis = key < S && (!CAUSAL || key <= qi);
-            p = vis ? p : 0.0f;
-            pv[u][r] = p;
-            dv4[u][r] = p * (pacc[r] - DLs[qi]);
-        }
-    }
-    __syncthreads();  // every wave is past its dP products: V's space is free
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int quad = w + 8 * u;
-        const int qm = quad >> 2, qn = quad & 3;
-        const int key = 16 * qn + l16;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int qi = 16 * qm + 4 * g4 + r;
-            PT[key * L::PSTR + qi] = pv[u][r];
-            DT[key * L::PSTR + qi] = dv4[u][r];
-        }
-    }
-    __syncthreads();
-
-    // ---- rows 32 rb.., columns 32 cb.. of dV, dK (rows: keys) and dQ (rows: queries) ----
     const int h32 = lane >> 5, l32 = lane & 31;
     const int rb = w >> 2;
     const int col = 32 * (w & 3) + l32;
     const int row = 32 * rb + l32;
-    f32x16 dv = zero16(), dk = zero16(), dq = zero16();
-    // k-steps s = 4t..4t+3 contract q = (s & 7) + 8 h32 + 16 (s >> 3); causal:
-    // keys 32.. (rb = 1) see queries >= 32 only (t >= 4), queries 0..31
-    // (rb = 0) see keys < 32 only (t < 4).
+
+    const int stride = (int)gridDim.x;
+    int bh = blockIdx.x;
+    prefetch(bh);
+    for (; bh < nbh; bh += stride) {
+        __syncthreads();  // the previous head's products are done with the tiles
+        {
+            float part = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const int q0 = 4 * (t & 1) + 8 * h32 + 16 * (t >> 1);
-        const bool kv_live = !CAUSAL || rb == 0 || t >= 4;
-        const bool q_live = !CAUSAL || rb == 1 || t < 4;
-        if (kv_live) {
-            const f32x4 pt = *(const f32x4 *)&PT[row * L::PSTR + q0];
-            const f32x4 dt = *(const f32x4 *)&DT[row * L::PSTR + q0];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                dv = mfma_32x32x2(pt[j], Gs[(q0 + j) * L::STR + col], dv);
-                dk = mfma_32x32x2(dt[j], Qs[(q0 + j) * L::STR + col], dk);
+            for (int c = 0; c < D / 32; ++c) {
+                const int off = j * L::STR + 32 * c + 4 * s8;
+                *(f32x4 *)&Qs[off] = rq[c];
+                *(f32x4 *)&Ks[off] = rk[c];
+                *(f32x4 *)&Vs[off] = rv[c];
+                *(f32x4 *)&Gs[off] = rg[c];
+                part += ro[c][0] * rg[c][0] + ro[c][1] * rg[c][1] + ro[c][2] * rg[c][2] + ro[c][3] * rg[c][3];
+            }
+            part += __shfl_xor(part, 1);
+            part += __shfl_xor(part, 2);
+            part += __shfl_xor(part, 4);
+            if (s8 == 0) {
+                L2s[j] = j < S ? lse_v * kLog2e : INFINITY;
+                DLs[j] = j < S ? part : 0.0f;
             }
         }
-        if (q_live) {
+        if (bh + stride < nbh) prefetch(bh + stride);
+        __syncthreads();
+
+        // ---- S, dP, P, dS of quadrants w and w + 8 ----
+        const int l16 = lane & 15, g4 = lane >> 4;
+        float pv[2][4], dv4[2][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                dq = mfma_32x32x2(DT[(q0 + j) * L::PSTR + row], Ks[(q0 + j) * L::STR + col], dq);
+        for (int u = 0; u < 2; ++u) {
+            const int quad = w + 8 * u;
+            const int qm = quad >> 2, qn = quad & 3;
+            const int key = 16 * qn + l16;
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+            if (!CAUSAL || qn <= qm) {
+                const int arow = (16 * qm + l16) * L::STR + 4 * g4;
+                const int brow = key * L::STR + 4 * g4;
+#pragma unroll
+                for (int c0 = 0; c0 < D; c0 += 16) {
+                    const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
+                    const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
+                    const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
+                    const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[jj], kf[jj], sacc, 0, 0, 0);
+                        pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[jj], vf[jj], pacc, 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qi = 16 * qm + 4 * g4 + r;
+                float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
+                const bool vis = key < S && (!CAUSAL || key <= qi);
+                p = vis ? p : 0.0f;
+                pv[u][r] = p;
+                dv4[u][r] = p * (pacc[r] - DLs[qi]);
+            }
         }
-    }
+        __syncthreads();  // every wave is past its dP products: V's space is free
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = 32 * rb + acc_row(i, h32);
-        if (r < S) {
-            const int64_t off = in_base + (int64_t)r * in_ss + col;
-            a.dv[off] = dv[i];
-            a.dk[off] = dk[i] * a.scale;
-            a.dq[off] = dq[i] * a.scale;
+        for (int u = 0; u < 2; ++u) {
+            const int quad = w + 8 * u;
+            const int qm = quad >> 2, qn = quad & 3;
+            const int key = 16 * qn + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qi = 16 * qm + 4 * g4 + r;
+                PT[key * L::PSTR + qi] = pv[u][r];
+                DT[key * L::PSTR + qi] = dv4[u][r];
+            }
+        }
+        __syncthreads();
+
+        // ---- rows 32 rb.., columns 32 cb.. of dV, dK (rows: keys) and dQ (rows: queries) ----
+        f32x16 dv = zero16(), dk = zero16(), dq = zero16();
+        auto kstep = [&](int t) {
+            const int q0 = 4 * (t & 1) + 8 * h32 + 16 * (t >> 1);
+            const bool kv_live = !CAUSAL || rb == 0 || t >= 4;
+            const bool q_live = !CAUSAL || rb == 1 || t < 4;
+            if (kv_live) {
+                const f32x4 pt = *(const f32x4 *)&PT[row * L::PSTR + q0];
+                const f32x4 dt = *(const f32x4 *)&DT[row * L::PSTR + q0];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    dv = mfma_32x32x2(pt[jj], Gs[(q0 + jj) * L::STR + col], dv);
+                    dk = mfma_32x32x2(dt[jj], Qs[(q0 + jj) * L::STR + col], dk);
+                }
+            }
+            if (q_live) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    dq = mfma_32x32x2(DT[(q0 + jj) * L::PSTR + row], Ks[(q0 + jj) * L::STR + col], dq);
+            }
+        };
+        // Half the k-steps unrolled, which keeps the kernel within 256
+        // registers next to the prefetched rows (fully unrolled, the
+        // non-causal kernel spills 12).
+#pragma unroll 4
+        for (int t = 0; t < 8; ++t) kstep(t);
+        const int64_t ib = in_base_of(bh);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = 32 * rb + acc_row(i, h32);
+            if (r < S) {
+                const int64_t off = ib + (int64_t)r * in_ss + col;
+                a.dv[off] = dv[i];
+                a.dk[off] = dk[i] * a.scale;
+                a.dq[off] = dq[i] * a.scale;
+            }
         }
     }
 }
 
 template <bool CAUSAL>
-int launch_bwd_short_lds64(const BwdArgs &args, int nbh)
+int launch_bwd_short_lds64p(const BwdArgs &args, int nbh)
 {
-    hipLaunchKernelGGL((attn_bwd_short_lds64<CAUSAL>), dim3((unsigned)nbh), dim3(512), 0, 0, args);
-    return launch_ok("attn_bwd_short_lds64") ? EMBER_OK : EMBER_ERR_DEVICE;
+    int ncu = 0;
+    const int st = device_cus(&ncu);
+    if (st != EMBER_OK) return st;
+    const int grid = nbh < ncu ? nbh : ncu;
+    hipLaunchKernelGGL((attn_bwd_short_lds64p<CAUSAL>), dim3((unsigned)grid), dim3(512), 0, 0, args, nbh);
+    return launch_ok("attn_bwd_short_lds64p") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
+
 
 // Short sequences at D <= 64 (S <= R, R = 32 or 64 rows): one workgroup of
 // R/8 waves per head, the head's Q, K, V, dO staged in LDS by direct copies
@@ -405,10 +455,19 @@ struct LdsBwdShape {
     static_assert(NQ * NW == (R / 16) * (R / 16) && NB * NW == 3 * NBO, "even split");
 };
 
+// R = 64 at D = 64 is persistent (one workgroup per CU walks heads
+// blockIdx.x, blockIdx.x + gridDim.x, ...), as attn_bwd_short_lds64p: each
+// thread prefetches its row share of the next head (Q, K, V, dO, O: 8 lanes
+// per row) into registers while the current head is multiplied, because the
+// 104 KB of LDS leave no room for a second workgroup to overlap the loads
+// (+11-15 % at S = 48 and 64).  At D = 32 (72 KB) two workgroups per CU
+// already overlap each other and the persistent form measured 0 to -6 %.
 template <int D, int R, bool CAUSAL>
-__global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs a)
+__global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs a, int nbh)
 {
     typedef LdsBwdShape<D, R> L;
+    constexpr bool kPersistent = R == 64 && D == 64;
+    constexpr int CH = D / 32;  // 16-byte chunks per lane and row
     __shared__ float tiles[4 * L::TILE];  // Q, K, V, dO
     __shared__ float PT[R * L::PSTR], DT[R * L::PSTR];
     __shared__ float L2s[R], DLs[R];
@@ -419,137 +478,186 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int bh = blockIdx.x;
-    const int b = bh / a.H;
-    const int hh = bh - b * a.H;
     const int S = a.S;
     const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
-    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
-    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
-
-    {
-        const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
-        const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
-        const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
-        const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
-#pragma unroll
-        for (int t = w; t < L::COP; t += L::NW) {
-            const int p = 64 * t + lane;
-            int r = p / L::ROWCH;
-            const int c = p - r * L::ROWCH;
-            const bool real = r < R && c < D / 4;
-            r = r < S ? r : S - 1;
-            const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
-            const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
-            dma16_buf(rq, oi, Qs + 256 * t);
-            dma16_buf(rk, oi, Ks + 256 * t);
-            dma16_buf(rv, oi, Vs + 256 * t);
-            dma16_buf(rg, og, Gs + 256 * t);
-        }
-    }
-    // Row statistics of rows 8w..8w+7, 8 lanes per row.
-    {
-        constexpr int CH = D / 32;  // 16-byte chunks per lane
-        const int j = 8 * w + (lane >> 3);
-        const int s8 = lane & 7;
-        const int jr = j < S ? j : S - 1;
-        const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
-        const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
-        float part = 0.0f;
-#pragma unroll
-        for (int it = 0; it < CH; ++it) {
-            const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
-            const f32x4 g4 = *(const f32x4 *)(grow + 32 * it + 4 * s8);
-            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
-        }
+    // Row statistics (and, persistent, staging): row j, 8 lanes per row.
+    const int j = 8 * w + (lane >> 3);
+    const int s8 = lane & 7;
+    const int jr = j < S ? j : S - 1;  // rows past S re-read row S-1 (masked later)
+    auto in_base_of = [&](int bh) {
+        const int b = bh / a.H;
+        return (int64_t)b * a.in_sb + (int64_t)(bh - b * a.H) * a.in_sh;
+    };
+    auto out_base_of = [&](int bh) {
+        const int b = bh / a.H;
+        return (int64_t)b * a.out_sb + (int64_t)(bh - b * a.H) * a.out_sh;
+    };
+    auto put_stats = [&](int bh, float part, float lse) {
         part += __shfl_xor(part, 1);
         part += __shfl_xor(part, 2);
         part += __shfl_xor(part, 4);
         if (s8 == 0) {
-            L2s[j] = j < S ? a.lse[(int64_t)bh * S + j] * kLog2e : INFINITY;
+            L2s[j] = j < S ? lse * kLog2e : INFINITY;
             DLs[j] = j < S ? part : 0.0f;
         }
-    }
-    wait_vmem();
-    __syncthreads();
+    };
 
     const int l16 = lane & 15, g4 = lane >> 4;
-    // ---- S, dP, P, dS of this wave's quadrants ----
+    // S / dP / P / dS of this wave's quadrants, then its 16 x 16 blocks of
+    // dV, dK, dQ, stored.  Q, K, V, dO and the statistics are in LDS.
+    auto compute = [&](int bh) {
+        const int64_t in_base = in_base_of(bh);
 #pragma unroll
-    for (int u = 0; u < L::NQ; ++u) {
-        const int quad = w + L::NW * u;
-        const int qm = quad / (R / 16), qn = quad - qm * (R / 16);
-        const int key = 16 * qn + l16;
-        f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
-        if (!CAUSAL || qn <= qm) {
-            const int arow = (16 * qm + l16) * L::STR + 4 * g4;
-            const int brow = key * L::STR + 4 * g4;
+        for (int u = 0; u < L::NQ; ++u) {
+            const int quad = w + L::NW * u;
+            const int qm = quad / (R / 16), qn = quad - qm * (R / 16);
+            const int key = 16 * qn + l16;
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
+            if (!CAUSAL || qn <= qm) {
+                const int arow = (16 * qm + l16) * L::STR + 4 * g4;
+                const int brow = key * L::STR + 4 * g4;
 #pragma unroll
-            for (int c0 = 0; c0 < D; c0 += 16) {
-                const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
-                const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
-                const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
-                const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
+                for (int c0 = 0; c0 < D; c0 += 16) {
+                    const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
+                    const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
+                    const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
+                    const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[j], kf[j], sacc, 0, 0, 0);
-                    pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[j], vf[j], pacc, 0, 0, 0);
+                    for (int jj = 0; jj < 4; ++jj) {
+                        sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[jj], kf[jj], sacc, 0, 0, 0);
+                        pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[jj], vf[jj], pacc, 0, 0, 0);
+                    }
                 }
             }
-        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int qi = 16 * qm + 4 * g4 + r;
-            float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
-            const bool vis = key < S && (!CAUSAL || key <= qi);
-            p = vis ? p : 0.0f;
-            PT[key * L::PSTR + qi] = p;
-            DT[key * L::PSTR + qi] = p * (pacc[r] - DLs[qi]);
+            for (int r = 0; r < 4; ++r) {
+                const int qi = 16 * qm + 4 * g4 + r;
+                float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
+                const bool vis = key < S && (!CAUSAL || key <= qi);
+                p = vis ? p : 0.0f;
+                PT[key * L::PSTR + qi] = p;
+                DT[key * L::PSTR + qi] = p * (pacc[r] - DLs[qi]);
+            }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // ---- this wave's 16 x 16 blocks of dV, dK, dQ ----
 #pragma unroll
-    for (int u = 0; u < L::NB; ++u) {
-        const int blk = w + L::NW * u;
-        const int o = blk / L::NBO;  // 0 dV, 1 dK, 2 dQ
-        const int rem = blk - o * L::NBO;
-        const int rb = rem / (D / 16), cb = rem - rb * (D / 16);
-        const int col = 16 * cb + l16;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (o < 2) {
-            // dV[k][n] = sum_q P^T[k][q] dO[q][n];  dK[k][n] = sum_q dS^T[k][q] Q[q][n]
-            const float *__restrict__ A = o == 0 ? PT : DT;
-            const float *__restrict__ Bt = o == 0 ? Gs : Qs;
+        for (int u = 0; u < L::NB; ++u) {
+            const int blk = w + L::NW * u;
+            const int o = blk / L::NBO;  // 0 dV, 1 dK, 2 dQ
+            const int rem = blk - o * L::NBO;
+            const int rb = rem / (D / 16), cb = rem - rb * (D / 16);
+            const int col = 16 * cb + l16;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (o < 2) {
+                // dV[k][n] = sum_q P^T[k][q] dO[q][n];  dK[k][n] = sum_q dS^T[k][q] Q[q][n]
+                const float *__restrict__ A = o == 0 ? PT : DT;
+                const float *__restrict__ Bt = o == 0 ? Gs : Qs;
 #pragma unroll
-            for (int c = 0; c < R / 16; ++c) {
-                if (CAUSAL && c < rb) continue;
-                const f32x4 af = *(const f32x4 *)&A[(16 * rb + l16) * L::PSTR + 16 * c + 4 * g4];
+                for (int c = 0; c < R / 16; ++c) {
+                    if (CAUSAL && c < rb) continue;
+                    const f32x4 af = *(const f32x4 *)&A[(16 * rb + l16) * L::PSTR + 16 * c + 4 * g4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[j], Bt[(16 * c + 4 * g4 + j) * L::STR + col],
-                                                              acc, 0, 0, 0);
-            }
-        } else {
-            // dQ[m][n] = sum_k dS[m][k] K[k][n] = sum_k dS^T[k][m] K[k][n]
+                    for (int jj = 0; jj < 4; ++jj)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            af[jj], Bt[(16 * c + 4 * g4 + jj) * L::STR + col], acc, 0, 0, 0);
+                }
+            } else {
+                // dQ[m][n] = sum_k dS[m][k] K[k][n] = sum_k dS^T[k][m] K[k][n]
 #pragma unroll
-            for (int c = 0; c < R / 16; ++c) {
-                if (CAUSAL && c > rb) continue;
+                for (int c = 0; c < R / 16; ++c) {
+                    if (CAUSAL && c > rb) continue;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int kk = 16 * c + 4 * g4 + j;
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(DT[kk * L::PSTR + 16 * rb + l16],
-                                                              Ks[kk * L::STR + col], acc, 0, 0, 0);
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const int kk = 16 * c + 4 * g4 + jj;
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(DT[kk * L::PSTR + 16 * rb + l16],
+                                                                  Ks[kk * L::STR + col], acc, 0, 0, 0);
+                    }
                 }
             }
-        }
-        float *__restrict__ dst = o == 0 ? a.dv : (o == 1 ? a.dk : a.dq);
-        const float mul = o == 0 ? 1.0f : a.scale;
+            float *__restrict__ dst = o == 0 ? a.dv : (o == 1 ? a.dk : a.dq);
+            const float mul = o == 0 ? 1.0f : a.scale;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * rb + 4 * g4 + r;
-            if (row < S) dst[in_base + (int64_t)row * in_ss + col] = acc[r] * mul;
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * rb + 4 * g4 + r;
+                if (row < S) dst[in_base + (int64_t)row * in_ss + col] = acc[r] * mul;
+            }
+        }
+    };
+
+    if constexpr (!kPersistent) {
+        const int bh = blockIdx.x;
+        const int64_t in_base = in_base_of(bh), out_base = out_base_of(bh);
+        {
+            const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
+            const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
+            const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
+            const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
+#pragma unroll
+            for (int t = w; t < L::COP; t += L::NW) {
+                const int p = 64 * t + lane;
+                int r = p / L::ROWCH;
+                const int c = p - r * L::ROWCH;
+                const bool real = r < R && c < D / 4;
+                r = r < S ? r : S - 1;
+                const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
+                const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
+                dma16_buf(rq, oi, Qs + 256 * t);
+                dma16_buf(rk, oi, Ks + 256 * t);
+                dma16_buf(rv, oi, Vs + 256 * t);
+                dma16_buf(rg, og, Gs + 256 * t);
+            }
+        }
+        {
+            const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
+            const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
+            float part = 0.0f;
+#pragma unroll
+            for (int it = 0; it < CH; ++it) {
+                const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
+                const f32x4 g4v = *(const f32x4 *)(grow + 32 * it + 4 * s8);
+                part += o4[0] * g4v[0] + o4[1] * g4v[1] + o4[2] * g4v[2] + o4[3] * g4v[3];
+            }
+            put_stats(bh, part, a.lse[(int64_t)bh * S + jr]);
+        }
+        wait_vmem();
+        __syncthreads();
+        compute(bh);
+    } else {
+        f32x4 rq[CH], rk[CH], rv[CH], rg[CH], ro[CH];
+        float lse_v = 0.0f;
+        auto prefetch = [&](int bh) {
+            const int64_t ib = in_base_of(bh) + (int64_t)jr * in_ss + 4 * s8;
+            const int64_t ob = out_base_of(bh) + (int64_t)jr * out_ss + 4 * s8;
+#pragma unroll
+            for (int it = 0; it < CH; ++it) {
+                rq[it] = *(const f32x4 *)(a.q + ib + 32 * it);
+                rk[it] = *(const f32x4 *)(a.k + ib + 32 * it);
+                rv[it] = *(const f32x4 *)(a.v + ib + 32 * it);
+                rg[it] = *(const f32x4 *)(a.dout + ob + 32 * it);
+                ro[it] = *(const f32x4 *)(a.o + ob + 32 * it);
+            }
+            lse_v = a.lse[(int64_t)bh * S + jr];
+        };
+        const int stride = (int)gridDim.x;
+        int bh = blockIdx.x;
+        prefetch(bh);
+        for (; bh < nbh; bh += stride) {
+            __syncthreads();  // the previous head's products are done with LDS
+            float part = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int off = j * L::STR + 32 * c + 4 * s8;
+                *(f32x4 *)&Qs[off] = rq[c];
+                *(f32x4 *)&Ks[off] = rk[c];
+                *(f32x4 *)&Vs[off] = rv[c];
+                *(f32x4 *)&Gs[off] = rg[c];
+                part += ro[c][0] * rg[c][0] + ro[c][1] * rg[c][1] + ro[c][2] * rg[c][2] + ro[c][3] * rg[c][3];
+            }
+            put_stats(bh, part, lse_v);
+            if (bh + stride < nbh) prefetch(bh + stride);
+            __syncthreads();
+            compute(bh);
         }
     }
 }
@@ -557,7 +665,14 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
 template <int D, int R, bool CAUSAL>
 int launch_bwd_lds16(const BwdArgs &args, int nbh)
 {
-    hipLaunchKernelGGL((attn_bwd_lds16<D, R, CAUSAL>), dim3((unsigned)nbh), dim3(R * 8), 0, 0, args);
+    int grid = nbh;
+    if (R == 64 && D == 64) {
+        int ncu = 0;
+        const int st = device_cus(&ncu);
+        if (st != EMBER_OK) return st;
+        grid = nbh < ncu ? nbh : ncu;
+    }
+    hipLaunchKernelGGL((attn_bwd_lds16<D, R, CAUSAL>), dim3((unsigned)grid), dim3(R * 8), 0, 0, args, nbh);
     return launch_ok("attn_bwd_lds16") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
@@ -631,11 +746,13 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     int st = check_attention_args(ptrs, 9, B, H, S, D, scale, strides, 6, who);
     if (st != EMBER_OK || B * H * S == 0) return st;
 
-    // S <= 64: one workgroup per head with its Q, K, V and dO staged in LDS,
-    // the row statistics formed in the kernel (no scratch, no atomics):
-    // attn_bwd_short_lds (S <= 32) and attn_bwd_short_lds64 at D = 128,
-    // attn_bwd_lds16 with 32- or 64-row tiles at D <= 64.  Measured with
-    // 2^20 query rows: 4.6-4.9 TB/s at S = 32 and 3.2-3.6 TB/s at S = 64,
+    // S <= 64: a workgroup stages one head's Q, K, V and dO in LDS and forms
+    // the row statistics itself (no scratch, no atomics):
+    // attn_bwd_short_lds (S <= 32) and attn_bwd_short_lds64p at D = 128,
+    // attn_bwd_lds16 with 32- or 64-row tiles at D <= 64; where a workgroup
+    // fills a CU's LDS (64-row tiles at D = 64 and 128) it is persistent
+    // and prefetches the next head into registers.  Measured with 2^20
+    // query rows: 4.6-4.9 TB/s at S = 32 and 3.7-4.3 TB/s at S = 64 (causal),
     // where the register-fed kernels they replaced (one wave per head or
     // per key block, rows read one per lane from HBM) moved 2.8-3.5 and
     // 2.0-2.1 TB/s.
@@ -675,8 +792,8 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
             case 11: return launch_bwd_lds16<32, 64, true>(sa, nbh);
             case 12: return launch_bwd_lds16<64, 64, false>(sa, nbh);
             case 13: return launch_bwd_lds16<64, 64, true>(sa, nbh);
-            case 16: return launch_bwd_short_lds64<false>(sa, nbh);
-            default: return launch_bwd_short_lds64<true>(sa, nbh);
+            case 16: return launch_bwd_short_lds64p<false>(sa, nbh);
+            default: return launch_bwd_short_lds64p<true>(sa, nbh);
         }
     }
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
