@@ -144,6 +144,12 @@ struct BwdLayout {
 
 constexpr int kMaxSlots = 5;  // BwdLayout<128>::SLOTS
 
+// Buffers for a block's dS: two at D = 64, used by alternate blocks, which
+// saves one barrier per block (bwd_step; +2-3 % at D = 64); one at D = 128
+// (no LDS left) and at D = 32 (two measured -1 to -4 % causal).
+template <int D>
+constexpr int kDsBufs = D == 64 ? 2 : 1;
+
 // Loop-invariant state of one workgroup.
 struct BwdBlock {
     const float *qp, *gp;      // q, dO at (b, h)
@@ -316,8 +322,9 @@ __device__ __forceinline__ void dq_softmax(const BwdArgs &a, const float *__rest
 //      the dQ MFMAs run, instead of leaving the matrix core idle;
 //   4. dQ of block qb-1 to global memory (atomics; DET: partial stores);
 //   5. dV += P^T dO, dK += dS^T Q of block qb;
-//   6. barrier (every wave has read dS of block qb-1), dS of block qb to
-//      LDS, wait for the copies, barrier.
+//   6. barrier (every wave has read dS of block qb-1; not needed with two
+//      dS buffers, see kDsBufs), dS of block qb to LDS, wait for the
+//      copies, barrier.
 // The mask is applied branch-free (an integer compare per element against a
 // per-lane threshold), so steps 2 and 3 are one basic block.  Keys a wave
 // cannot see in this block (causal, above the diagonal) get P = 0 by the same
@@ -326,7 +333,8 @@ template <int D, bool CAUSAL, bool PREV, bool MASK, bool DET>
 __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, int qb,
                                          const float *__restrict__ qs,
                                          const float *__restrict__ gs,
-                                         const float *__restrict__ st, float *__restrict__ ds,
+                                         const float *__restrict__ st, float *__restrict__ dsb,
+                                         int parity,
                                          float *__restrict__ qn, float *__restrict__ gn,
                                          float *__restrict__ stn,
                                          const float *__restrict__ kall, const float *kr,
@@ -340,6 +348,11 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
     const int m0 = qb * kBq;
+    // dS buffers (kDsBufs): this block's dS goes to buffer `parity`, the
+    // previous block's is read from the other one (the same one at D = 128).
+    constexpr int kDsStride = (kDsBufs<D> - 1) * kBq * L::SSTR;
+    const float *const ds = dsb + (parity ^ 1) * kDsStride;
+    float *const ds_out = dsb + parity * kDsStride;
 
     if (qb + 1 < k.nq) bwd_fetch<D>(k, m0 + kBq, qn, gn, stn);
 
@@ -405,12 +418,14 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
             }
         }
     }
-    // Every wave has read the previous block's dS.
-    __syncthreads();
+    // Every wave has read the previous block's dS (with one dS buffer; with
+    // two, this block's dS goes to the other one, which nobody has read since
+    // the last step's closing barrier).
+    if constexpr (kDsBufs<D> == 1) __syncthreads();
     {
         const int sbase = 4 * h32 * L::SSTR + kBkw * k.w + l32;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ds[sbase + ((i >> 2) * 8 + (i & 3)) * L::SSTR] = pacc[i];
+        for (int i = 0; i < 16; ++i) ds_out[sbase + ((i >> 2) * 8 + (i & 3)) * L::SSTR] = pacc[i];
     }
     wait_vmem();  // this wave's copies into (qn, gn, stn) have landed
     __syncthreads();
@@ -445,7 +460,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     __shared__ float Qs0[L::QBUF], Qs1[L::QBUF];
     __shared__ float dOs0[L::QBUF], dOs1[L::QBUF];
     __shared__ float St0[2 * kBq], St1[2 * kBq];
-    __shared__ float dSs[kBq * L::SSTR];
+    __shared__ float dSs[kDsBufs<D> * kBq * L::SSTR];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -540,13 +555,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     const int tail_bias = k.n0w + l32 >= S ? (1 << 24) : 0;
     auto walk = [&](auto mask) {
         constexpr bool M = decltype(mask)::value;
-        bwd_step<D, CAUSAL, false, M, DET>(a, k, qstart, Qs0, dOs0, St0, dSs, Qs1, dOs1, St1, Kall,
+        bwd_step<D, CAUSAL, false, M, DET>(a, k, qstart, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1, Kall,
                                            kr, vr, dvacc, dkacc, tail_bias);
         for (int qb = qstart + 1; qb < k.nq; qb += 2) {
-            bwd_step<D, CAUSAL, true, M, DET>(a, k, qb, Qs1, dOs1, St1, dSs, Qs0, dOs0, St0, Kall,
+            bwd_step<D, CAUSAL, true, M, DET>(a, k, qb, Qs1, dOs1, St1, dSs, 1, Qs0, dOs0, St0, Kall,
                                               kr, vr, dvacc, dkacc, tail_bias);
             if (qb + 1 < k.nq)
-                bwd_step<D, CAUSAL, true, M, DET>(a, k, qb + 1, Qs0, dOs0, St0, dSs, Qs1, dOs1,
+                bwd_step<D, CAUSAL, true, M, DET>(a, k, qb + 1, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1,
                                                   St1, Kall, kr, vr, dvacc, dkacc, tail_bias);
         }
     };
@@ -554,7 +569,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
         walk(std::true_type{});
     else
         walk(std::false_type{});
-    bwd_last_dq<D, DET>(a, k, (k.nq - 1) * kBq, dSs, Kall);
+    bwd_last_dq<D, DET>(a, k, (k.nq - 1) * kBq,
+                        dSs + ((k.nq - 1 - qstart) & 1) * (kDsBufs<D> - 1) * kBq * L::SSTR, Kall);
 
     // dK (scaled) and dV rows of this wave's keys: register i -> key
     // n0w + acc_row(i, h32), lane -> d = DB*l32 + db.
