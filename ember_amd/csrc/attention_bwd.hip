@@ -14,7 +14,6 @@
 // D = 128, while for non-causal D = 128 the default allocation cycles the
 // 128 dK/dV accumulators between AGPRs and VGPRs every query block and runs
 // 2x slower than the VGPR form (and D = 64 causal is 6 % faster in VGPR form).
-#include <atomic>
 #include <mutex>
 
 #include "attention_bwd_kernels.h"
@@ -22,26 +21,12 @@
 namespace ember {
 namespace {
 
-// Compute units of the current device (cached per device): the grid of the
-// persistent kernels below.
+// Compute units of the current device: the grid of the persistent kernels
+// below.
 int device_cus(int *out)
 {
-    constexpr int kDevices = 16;
-    static std::atomic<int> cached[kDevices];
-    int dev = 0;
-    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return EMBER_ERR_DEVICE;
-    if (dev >= 0 && dev < kDevices && cached[dev].load() > 0) {
-        *out = cached[dev].load();
-        return EMBER_OK;
-    }
-    int n = 0;
-    if (!hip_ok(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
-                "hipDeviceGetAttribute"))
-        return EMBER_ERR_DEVICE;
-    n = n > 0 ? n : 1;
-    if (dev >= 0 && dev < kDevices) cached[dev].store(n);
-    *out = n;
-    return EMBER_OK;
+    *out = device_cu_count();
+    return *out > 0 ? EMBER_OK : record_error(EMBER_ERR_DEVICE, "hipDeviceGetAttribute(CU count)");
 }
 
 // Short sequences at D = 128 (S <= 32): one workgroup of 4 waves per head,

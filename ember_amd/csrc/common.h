@@ -39,4 +39,8 @@ enum ScratchSlot {
 // The library-wide switch set by ember_set_deterministic.
 bool deterministic();
 
+// Compute units of the current device (cached per device), or 0 if the HIP
+// runtime cannot say; records no error.
+int device_cu_count();
+
 }  // namespace ember

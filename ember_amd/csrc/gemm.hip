@@ -543,19 +543,11 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmArgs g, int ksplit
     }
 }
 
-int g_num_cus[16];
-
+// Tile-shape choice only: an unknown CU count falls back to MI355X's 256.
 int num_cus()
 {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
-    if (g_num_cus[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-        g_num_cus[dev] = n;
-    }
-    return g_num_cus[dev];
+    const int n = device_cu_count();
+    return n > 0 ? n : 256;
 }
 
 template <bool TA, bool TB>

@@ -115,7 +115,23 @@ void release_scratch(int dev)
 
 namespace {
 std::atomic<int> g_deterministic{0};
+std::atomic<int> g_cu_count[kMaxDevices];
 }  // namespace
+
+int device_cu_count()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (dev >= 0 && dev < kMaxDevices) {
+        const int c = g_cu_count[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        return 0;
+    if (dev >= 0 && dev < kMaxDevices) g_cu_count[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
 
 bool deterministic()
 {
