@@ -784,9 +784,14 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
     const int64_t nkb = (S + kBk - 1) / kBk;
+    // S <= 128 at D = 128: one workgroup holds all of a head's keys and each
+    // wave all of them for its 32 columns of dQ, so the kernel forms the row
+    // statistics itself and stores dQ directly (no attn_bwd_pre, no scratch,
+    // no atomics; reproducible as is).
+    const bool solo = D == 128 && nkb == 1;
     // Deterministic dq: per-key-block partials, summed in a fixed order.
     float *dq_part = nullptr;
-    if (deterministic()) {
+    if (!solo && deterministic()) {
         if (noalloc)
             return record_error(EMBER_ERR_UNSUPPORTED,
                                 "attention_bwd_noalloc: deterministic dq at S > 64 needs a scratch "
@@ -800,8 +805,10 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
         if (!dq_part) return EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
     }
     float *stats = nullptr;
-    st = stats_source(rows_pad, &stats);
-    if (st != EMBER_OK) return st;
+    if (!solo) {
+        st = stats_source(rows_pad, &stats);
+        if (st != EMBER_OK) return st;
+    }
 
     BwdArgs args;
     args.q = q;
@@ -813,8 +820,8 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.dq = dq;
     args.dk = dk;
     args.dv = dv;
-    args.lse2 = stats;
-    args.delta = stats + rows_pad;
+    args.lse2 = stats;  // null: statistics formed in the kernel (launch_bwd)
+    args.delta = stats ? stats + rows_pad : nullptr;
     args.dq_part = dq_part;
     args.H = (int)H;
     args.S = (int)S;

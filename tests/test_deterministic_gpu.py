@@ -14,7 +14,8 @@ from 65 (one key block with a tail) to 4096 (32 key blocks):
 * the Python front end (ember_amd.set_deterministic + attention_backward)
   takes the same path.
 S <= 64 has no atomics in either mode; one such case checks that the
-switch leaves it bitwise alone.
+switch leaves it bitwise alone.  S <= 128 at D = 128 (the direct-dQ kernel,
+one store per element) is reproducible in both modes and is among the cases.
 """
 
 import numpy as np
@@ -79,6 +80,7 @@ CASES = [
     (2, 2, 129, 128, False, [12, 4], [0, 3]),
     (3, 5, 1000, 64, True, [0, 0], [0, 0]),
     (1, 1, 65, 32, False, [0, 0], [0, 0]),
+    (3, 3, 100, 128, True, [4, 0], [0, 1]),      # S <= 128 at D = 128: the direct-dQ kernel
     (2, 16, 1024, 64, True, [0, 0], [0, 0]),     # config 5's shape per head, 32 heads
 ]
 
