@@ -84,18 +84,26 @@ def test_random_short_sequence_many_heads(seed):
     _run(200 + seed, *_short_case(seed))
 
 
-@pytest.mark.parametrize("B,H,S,causal,pads,hpads", [
-    (1, 257, 32, False, [0, 0], [0, 0]),
-    (3, 171, 9, True, [4, 12], [1, 0]),
-    (5, 206, 32, True, [0, 32], [3, 1]),
-    (8, 128, 32, False, [12, 4], [0, 3]),
-    (16, 160, 31, False, [0, 0], [0, 0]),
+@pytest.mark.parametrize("B,H,S,D,causal,pads,hpads", [
+    (1, 257, 32, 128, False, [0, 0], [0, 0]),
+    (3, 171, 9, 128, True, [4, 12], [1, 0]),
+    (5, 206, 32, 128, True, [0, 32], [3, 1]),
+    (8, 128, 32, 128, False, [12, 4], [0, 3]),
+    (16, 160, 31, 128, False, [0, 0], [0, 0]),
+    (1, 257, 64, 128, True, [0, 0], [0, 0]),
+    (3, 171, 48, 128, False, [4, 12], [1, 0]),
+    (10, 256, 64, 128, False, [0, 4], [0, 1]),
+    (1, 300, 64, 64, True, [0, 0], [0, 0]),
+    (5, 206, 33, 64, False, [12, 4], [3, 0]),
+    (16, 160, 64, 64, True, [4, 0], [0, 2]),
 ])
-def test_short_backward_walks_many_heads(B, H, S, causal, pads, hpads):
-    """S <= 32 at D = 128 with hundreds to thousands of one-head workgroups
-    (257 to 2560 heads, ragged S), padded strides on both triples: the
-    workgroups that share a CU must not disturb each other's LDS tiles."""
-    _run(300 + B + H + S, B, H, S, 128, causal, pads, hpads)
+def test_short_backward_walks_many_heads(B, H, S, D, causal, pads, hpads):
+    """S <= 64 with hundreds to thousands of heads (257 to 2560, ragged S),
+    padded strides on both triples: at S <= 32 the one-head workgroups that
+    share a CU must not disturb each other's LDS tiles; at 32 < S <= 64 with
+    D = 64 or 128 one persistent workgroup per CU walks several heads, each
+    prefetched during the previous one (a ragged last pass included)."""
+    _run(300 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 
 def _run(seed, B, H, S, D, causal, pads, hpads):
