@@ -200,7 +200,7 @@ extern "C" int adam_step(float *const *params, const float *const *grads, float 
     if (st != EMBER_OK) return st;
     if (step < 1) return record_error(EMBER_ERR_INVALID_ARGUMENT, "adam_step");
     return launch_opt<Rule::kAdam>(params, grads, exp_avg, exp_avg_sq, sizes, ntensors,
-                                   adam_scalars(lr, beta1, beta2, eps, step), "adam_kernel");
+                                   adam_scalars(lr, beta1, beta2, eps, step), "adam_step");
 }
 
 extern "C" int adamw_step(float *const *params, const float *const *grads, float *const *exp_avg,
@@ -214,7 +214,7 @@ extern "C" int adamw_step(float *const *params, const float *const *grads, float
     OptScalars s = adam_scalars(lr, beta1, beta2, eps, step);
     s.lrwd = (float)(lr * weight_decay);
     return launch_opt<Rule::kAdamW>(params, grads, exp_avg, exp_avg_sq, sizes, ntensors, s,
-                                    "adamw_kernel");
+                                    "adamw_step");
 }
 
 extern "C" int sgd_step(float *const *params, const float *const *grads, float *const *velocity,
@@ -226,5 +226,5 @@ extern "C" int sgd_step(float *const *params, const float *const *grads, float *
     OptScalars s{};
     s.lr = (float)lr;
     s.momentum = (float)momentum;
-    return launch_opt<Rule::kSgd>(params, grads, velocity, nullptr, sizes, ntensors, s, "sgd_kernel");
+    return launch_opt<Rule::kSgd>(params, grads, velocity, nullptr, sizes, ntensors, s, "sgd_step");
 }
