@@ -511,6 +511,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     if constexpr (!kSolo) {
         k.l2p = a.lse2 + (int64_t)bh * a.S_pad;
         k.dlp = a.delta + (int64_t)bh * a.S_pad;
+    } else {
+        k.l2p = k.dlp = nullptr;  // statistics live in SoloSt
     }
     if constexpr (DQ == kDqPartial)
         k.dqp = a.dq_part + ((int64_t)(kb * L::NSPLIT + w / DB) * BH + bh) * a.S_pad * D;
