@@ -348,6 +348,40 @@ def test_long_sequence_against_float64(S, D, causal):
         np.testing.assert_allclose(dk[0, 0, j], scale * (ds @ q64[i0:]), err_msg=f"dK row {j}", **TOL)
 
 
+@pytest.mark.parametrize("S,D", [(131072, 64), (65536, 128)])
+def test_very_long_sequence_sampled_rows(S, D):
+    """One causal head of 64k-128k rows, beyond the oracle's reach: O and
+    LSE of sampled rows against float64 (each an O(S D) sum), and the
+    backward's contract on sampled rows and keys in float64 from the given O
+    and LSE (P = exp(scale q.k - LSE), Delta = dO.O): dQ rows, dK and dV
+    keys.  The row, block and statistic offsets here exceed 2^22 elements
+    per tensor, the largest index products of any test."""
+    q, k, v, d_o = _inputs(1, 1, S, D, seed=1300 + D)
+    scale = G.scale_for(D)
+    o, lse = G.attention_fwd(q, k, v, True)
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, True)
+    q64, k64, v64, g64 = (x[0, 0].astype(np.float64) for x in (q, k, v, d_o))
+    o64, lse64 = o[0, 0].astype(np.float64), lse[0, 0].astype(np.float64)
+    delta = (g64 * o64).sum(axis=1)
+    picks = sorted({0, 1, 127, 128, S // 2 - 1, S // 2, S - 129, S - 2, S - 1}
+                   | set(np.random.default_rng(S + D).choice(S, 8, replace=False).tolist()))
+    for i in picks:
+        sc = scale * (k64[:i + 1] @ q64[i])
+        m = sc.max()
+        w = np.exp(sc - m)
+        ref_lse = m + np.log(w.sum())
+        np.testing.assert_allclose(lse[0, 0, i], ref_lse, err_msg=f"LSE row {i}", **TOL)
+        np.testing.assert_allclose(o[0, 0, i], (w @ v64[:i + 1]) / w.sum(), err_msg=f"O row {i}", **TOL)
+        p = np.exp(sc - lse64[i])
+        ds = p * (v64[:i + 1] @ g64[i] - delta[i])
+        np.testing.assert_allclose(dq[0, 0, i], scale * (ds @ k64[:i + 1]), err_msg=f"dQ row {i}", **TOL)
+    for j in picks:
+        p = np.exp(scale * (q64[j:] @ k64[j]) - lse64[j:])
+        ds = p * (g64[j:] @ v64[j] - delta[j:])
+        np.testing.assert_allclose(dv[0, 0, j], p @ g64[j:], err_msg=f"dV row {j}", **TOL)
+        np.testing.assert_allclose(dk[0, 0, j], scale * (ds @ q64[j:]), err_msg=f"dK row {j}", **TOL)
+
+
 @pytest.mark.parametrize("D,causal", [(128, True), (64, False)])
 def test_known_answers_at_full_length(D, causal):
     """Closed forms at S = 4096 on the HIP kernels themselves: K = 0 makes
