@@ -348,6 +348,63 @@ def test_long_sequence_against_float64(S, D, causal):
         np.testing.assert_allclose(dk[0, 0, j], scale * (ds @ q64[i0:]), err_msg=f"dK row {j}", **TOL)
 
 
+def _check_against_oracle(q, k, v, d_o, causal, scale, grad_atol):
+    o, lse = G.attention_fwd(q, k, v, causal, scale)
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, causal, scale)
+    np.testing.assert_allclose(o, o_ref, **TOL)
+    np.testing.assert_allclose(lse, lse_ref, rtol=1e-5, atol=2e-4)
+    grads = G.attention_bwd(q, k, v, o, lse, d_o, causal, scale)
+    refs = oracle.attention_bwd(q, k, v, o_ref, lse_ref, d_o, causal, scale)
+    for name, got, ref in zip(("dq", "dk", "dv"), grads, refs):
+        assert np.isfinite(got).all(), name
+        G.say(f"  {name}: max |err| {float(np.max(np.abs(got - ref))):.3g} (atol {grad_atol:.3g})")
+        np.testing.assert_allclose(got, ref, rtol=1e-3, atol=grad_atol, err_msg=f"{name} scale={scale}")
+    return lse
+
+
+@pytest.mark.parametrize("S,D,causal", [(1024, 128, True), (513, 128, False), (300, 64, True), (64, 64, True),
+                                         (200, 32, False)])
+def test_running_max_climbs_along_the_keys(S, D, causal):
+    """Key j carries a component (32 j / S) u along a direction u that every
+    query shares, so each row's maximum score climbs by ~32 (natural log
+    units) over the keys: the running maximum, which the forward raises
+    lazily (only when a score exceeds it by more than 2^8 in base 2, i.e.
+    5.5), is raised five or more times along a full row, and a wrong rescale
+    of O or of the running sum would show at once.  Scores stay within
+    ~+-40, so the north-star tolerance applies unchanged."""
+    q, k, v, d_o = _inputs(1, 2, S, D, seed=1400 + S + D)
+    u = np.ones(D, np.float32) / np.sqrt(D)
+    q = (q + 4.0 * u).astype(np.float32)                    # q . u ~ 4
+    k = (k + (8.0 * np.arange(S) / S)[:, None].astype(np.float32) * u * np.sqrt(D)).astype(np.float32)
+    G.say(f"climbing max S={S} D={D} causal={causal}")
+    _check_against_oracle(q, k, v, d_o, causal, G.scale_for(D), 2e-4)
+
+
+@pytest.mark.parametrize("S,D,causal", [(1024, 128, True), (513, 128, False), (200, 32, False)])
+def test_peaked_scores_and_zero_scale(S, D, causal):
+    """Scale 1 with q, k ~ N(0, 4): scores with a standard deviation of
+    sigma = 4 sqrt(D) (up to ~+-200), softmax rows close to one-hot.  O and
+    LSE are held to the north-star tolerance.  The gradients' absolute
+    tolerance is the north star's times sigma: the backward recomputes each
+    score in fp32, with an absolute rounding of order |s| D 2^-24 that
+    perturbs P relatively by as much, and dK, dQ sum such terms against
+    Q, K of magnitude 2 (measured: 0.9e-3 to 1.6e-3 worst absolute error
+    in dQ and dK at D = 128, against 2e-4 sigma = 9e-3; 1e-5 to 5e-5 in the
+    climbing-maximum test above, at ordinary score magnitudes).  Then
+    scale 0: every visible key gets exactly the same weight
+    (LSE = ln(count)), at the north star."""
+    q, k, v, d_o = _inputs(1, 2, S, D, seed=1500 + S + D)
+    q, k = 2.0 * q, 2.0 * k
+    sigma = 4.0 * np.sqrt(D)
+    G.say(f"peaked scores S={S} D={D} causal={causal}")
+    _check_against_oracle(q, k, v, d_o, causal, 1.0, 2e-4 * sigma)
+    G.say(f"zero scale S={S} D={D} causal={causal}")
+    lse = _check_against_oracle(q, k, v, d_o, causal, 0.0, 2e-4)
+    n = np.arange(1, S + 1) if causal else np.full(S, S)
+    np.testing.assert_allclose(lse[0, 0], np.log(n), rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("S,D", [(131072, 64), (65536, 128)])
 def test_very_long_sequence_sampled_rows(S, D):
     """One causal head of 64k-128k rows, beyond the oracle's reach: O and
