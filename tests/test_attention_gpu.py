@@ -405,6 +405,32 @@ def test_peaked_scores_and_zero_scale(S, D, causal):
     np.testing.assert_allclose(lse[0, 0], np.log(n), rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("B,H,S,D,causal", [
+    (64, 64, 128, 128, True),    # direct-dQ workgroup kernel, 4096 heads
+    (32, 64, 130, 64, False),    # two key blocks, atomic dQ, 2048 heads
+    (128, 64, 64, 128, True),    # persistent S <= 64 kernel, 8192 heads
+    (256, 64, 32, 64, False),    # one-head LDS workgroups, 16384 heads
+])
+def test_many_heads_sampled(B, H, S, D, causal):
+    """The bench's short-sequence scale (2^19-2^20 query rows, thousands of
+    heads): every output finite, and the first, a middle and the last head
+    against the oracle."""
+    rng = np.random.default_rng(1600 + S + D)
+    q, k, v, d_o = (rng.standard_normal((B, H, S, D), dtype=np.float32) for _ in range(4))
+    o, lse = G.attention_fwd(q, k, v, causal)
+    grads = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    assert all(np.isfinite(g).all() for g in grads)
+    for b, h in ((0, 0), (B // 2, H // 3), (B - 1, H - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_ref, lse_ref = oracle.attention_fwd(q[sl], k[sl], v[sl], causal)
+        np.testing.assert_allclose(o[sl], o_ref, err_msg=f"O b={b} h={h}", **TOL)
+        np.testing.assert_allclose(lse[sl], lse_ref, err_msg=f"LSE b={b} h={h}", **TOL)
+        refs = oracle.attention_bwd(q[sl], k[sl], v[sl], o_ref, lse_ref, d_o[sl], causal)
+        for name, got, ref in zip(("dQ", "dK", "dV"), grads, refs):
+            np.testing.assert_allclose(got[sl], ref, err_msg=f"{name} b={b} h={h}", **TOL)
+
+
 @pytest.mark.parametrize("S,D", [(131072, 64), (65536, 128)])
 def test_very_long_sequence_sampled_rows(S, D):
     """One causal head of 64k-128k rows, beyond the oracle's reach: O and
