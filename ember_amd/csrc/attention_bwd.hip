@@ -310,7 +310,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
         float pv[2][4], dv4[2][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int quad = w + 8 * u;
+            const int quad = w + L::NW * u;
             const int qm = quad >> 2, qn = quad & 3;
             const int key = 16 * qn + l16;
             f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
         __syncthreads();  // every wave is past its dP products: V's space is free
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int quad = w + 8 * u;
+            const int quad = w + L::NW * u;
             const int qm = quad >> 2, qn = quad & 3;
             const int key = 16 * qn + l16;
 #pragma unroll
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
         const int b = bh / a.H;
         return (int64_t)b * a.out_sb + (int64_t)(bh - b * a.H) * a.out_sh;
     };
-    auto put_stats = [&](int bh, float part, float lse) {
+    auto put_stats = [&](float part, float lse) {
         part += __shfl_xor(part, 1);
         part += __shfl_xor(part, 2);
         part += __shfl_xor(part, 4);
@@ -579,7 +579,9 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
             const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
             const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
 #pragma unroll
-            for (int t = w; t < L::COP; t += L::NW) {
+            for (int sl = 0; sl < (L::COP + L::NW - 1) / L::NW; ++sl) {  // copy t = w + NW sl
+                const int t = w + L::NW * sl;
+                if (t >= L::COP) break;
                 const int p = 64 * t + lane;
                 int r = p / L::ROWCH;
                 const int c = p - r * L::ROWCH;
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
                 const f32x4 g4v = *(const f32x4 *)(grow + 32 * it + 4 * s8);
                 part += o4[0] * g4v[0] + o4[1] * g4v[1] + o4[2] * g4v[2] + o4[3] * g4v[3];
             }
-            put_stats(bh, part, a.lse[(int64_t)bh * S + jr]);
+            put_stats(part, a.lse[(int64_t)bh * S + jr]);
         }
         wait_vmem();
         __syncthreads();
@@ -639,7 +641,7 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
                 *(f32x4 *)&Gs[off] = rg[c];
                 part += ro[c][0] * rg[c][0] + ro[c][1] * rg[c][1] + ro[c][2] * rg[c][2] + ro[c][3] * rg[c][3];
             }
-            put_stats(bh, part, lse_v);
+            put_stats(part, lse_v);
             if (bh + stride < nbh) prefetch(bh + stride);
             __syncthreads();
             compute(bh);
