@@ -418,8 +418,9 @@ def synchronize() -> None:
 
 
 def empty_cache() -> None:
-    """Returns the device allocator's cached (freed) blocks to HIP; the next
-    allocations call hipMalloc again."""
+    """Returns the device allocator's cached (freed) blocks and the library's
+    scratch buffers to HIP; the next allocations call hipMalloc again.  Call
+    it when no other thread is inside the library."""
     C._empty_cache()
 
 

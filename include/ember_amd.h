@@ -58,8 +58,10 @@ void sync_device(void);
  * ember_empty_cache synchronises the current device and hipFrees every
  * cached block and the library's own scratch buffers (attention_bwd's row
  * statistics and dq partials, reduction partials), which are otherwise kept
- * for reuse; ember_memory_stats gives the current device's bytes handed
- * out, bytes cached and peak bytes handed out (rounded block sizes). */
+ * for reuse; call it when no other thread is inside the library (a call in
+ * flight may hold a scratch buffer it has not launched on yet).
+ * ember_memory_stats gives the current device's bytes handed out, bytes
+ * cached and peak bytes handed out (rounded block sizes). */
 void ember_empty_cache(void);
 void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak);
 
