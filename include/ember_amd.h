@@ -12,6 +12,13 @@
  * default-stream launches; results are visible after sync_device() or a
  * copy_from_device(), which synchronises.
  *
+ * Threads.  Like the reference (single-threaded, every call made under the
+ * Python GIL), the library expects one host thread in it at a time per
+ * device: operators that use library scratch (attention_bwd's row
+ * statistics, split-K and reduction partials) share one buffer per device
+ * and operator, and two threads' launches may interleave on the null
+ * stream.  The allocator and the error slots are thread-safe.
+ *
  * Error behaviour.  The reference prints and calls exit() on any device
  * error (src/core/utils_gpu.cuh:13-19).  Here the void entry points keep
  * their signatures but record the first error in a sticky per-thread slot
