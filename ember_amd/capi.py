@@ -98,7 +98,7 @@ def lib() -> C.CDLL:
 def set_deterministic(enabled: bool) -> None:
     """Process-wide switch for bitwise-reproducible results
     (ember_set_deterministic).  Off by default.  With it on, attention_bwd's
-    dq at S > 64 is summed in a fixed key order (a scratch buffer of
+    dq at S > 128 (S > 64 at D = 32) is summed in a fixed key order (a scratch buffer of
     ceil(S/128)*B*H*S_pad*128 floats and one extra pass) instead of with
     atomic adds; every other operator is reproducible either way."""
     lib().ember_set_deterministic(1 if enabled else 0)

@@ -742,8 +742,11 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     // query rows: 4.6-4.9 TB/s at S = 32 and 3.7-4.3 TB/s at S = 64 (causal),
     // where the register-fed kernels they replaced (one wave per head or
     // per key block, rows read one per lane from HBM) moved 2.8-3.5 and
-    // 2.0-2.1 TB/s.
-    if (S <= 2 * kBq) {
+    // 2.0-2.1 TB/s.  64 < S <= 128 at D = 64 and 128: attn_bwd_s128, one
+    // workgroup per head with 16-key chunks dealt out so that a causal
+    // head's waves have equal work, the row statistics formed in the kernel
+    // and dQ stored directly (no scratch, no atomics, reproducible).
+    if (S <= 2 * kBq || (S <= kBk && D >= 64)) {
         BwdArgs sa;
         sa.q = q;
         sa.k = k;
@@ -767,6 +770,7 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
         sa.out_sh = out_sh;
         sa.out_ss = out_ss;
         const int nbh = (int)(B * H);
+        if (S > 2 * kBq) return launch_bwd_s128(sa, (int)D, causal != 0, nbh);
         const int key = (S <= kBq ? 0 : 8) + (int)(D / 32) * 2 + (causal ? 1 : 0);
         switch (key) {
             case 2: return launch_bwd_lds16<32, 32, false>(sa, nbh);
@@ -786,18 +790,13 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
     const int64_t nkb = (S + kBk - 1) / kBk;
-    // S <= 128 at D = 128: one workgroup holds all of a head's keys and each
-    // wave all of them for its 32 columns of dQ, so the kernel forms the row
-    // statistics itself and stores dQ directly (no attn_bwd_pre, no scratch,
-    // no atomics; reproducible as is).
-    const bool solo = D == 128 && nkb == 1;
     // Deterministic dq: per-key-block partials, summed in a fixed order.
     float *dq_part = nullptr;
-    if (!solo && deterministic()) {
+    if (deterministic()) {
         if (noalloc)
             return record_error(EMBER_ERR_UNSUPPORTED,
-                                "attention_bwd_noalloc: deterministic dq at S > 64 needs a scratch "
-                                "buffer (use attention_bwd)");
+                                "attention_bwd_noalloc: deterministic dq at S > 128 (S > 64 at D = 32) "
+                                "needs a scratch buffer (use attention_bwd)");
         // B*H*S_pad*128*4 < 2^61 (B*H < 2^21, S < 2^30): the product below
         // cannot wrap once nkb passes this check.
         if (nkb > INT64_MAX / (B * H * S_pad * kBk * (int64_t)sizeof(float)))
@@ -807,10 +806,8 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
         if (!dq_part) return EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
     }
     float *stats = nullptr;
-    if (!solo) {
-        st = stats_source(rows_pad, &stats);
-        if (st != EMBER_OK) return st;
-    }
+    st = stats_source(rows_pad, &stats);
+    if (st != EMBER_OK) return st;
 
     BwdArgs args;
     args.q = q;
@@ -822,8 +819,8 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.dq = dq;
     args.dk = dk;
     args.dv = dv;
-    args.lse2 = stats;  // null: statistics formed in the kernel (launch_bwd)
-    args.delta = stats ? stats + rows_pad : nullptr;
+    args.lse2 = stats;
+    args.delta = stats + rows_pad;
     args.dq_part = dq_part;
     args.H = (int)H;
     args.S = (int)S;

@@ -79,6 +79,11 @@ struct BwdArgs {
 // its own, see the file comment).
 int launch_bwd_causal_d128(const BwdArgs &args, int64_t rows_pad, int nblocks);
 
+// attention_bwd_s128.hip: 64 < S <= 128 at D = 64 or 128, one workgroup
+// per head (no row statistics or dq partials: args.lse2, delta, dq_part
+// unused).
+int launch_bwd_s128(const BwdArgs &args, int D, bool causal, int nbh);
+
 namespace {
 
 constexpr int kWaves = 4;
@@ -147,12 +152,8 @@ constexpr int kMaxSlots = 5;  // BwdLayout<128>::SLOTS
 // How a workgroup's dQ reaches memory:
 //   kDqAtomic: added into dq with fp32 atomics (dq zeroed by attn_bwd_pre);
 //   kDqPartial: stored into the wave's partial slab (deterministic mode),
-//     summed by attn_bwd_dq_reduce;
-//   kDqDirect: stored into dq; only when one workgroup holds all of a head's
-//     keys (S <= 128) and each wave all of them for its d columns (D = 128),
-//     so its block is complete.  This mode also forms the row statistics in
-//     the kernel (no attn_bwd_pre, no scratch).
-constexpr int kDqAtomic = 0, kDqPartial = 1, kDqDirect = 2;
+//     summed by attn_bwd_dq_reduce.
+constexpr int kDqAtomic = 0, kDqPartial = 1;
 
 // Buffers for a block's dS: two at D = 64, used by alternate blocks, which
 // saves one barrier per block (bwd_step; +2-3 % at D = 64); one at D = 128
@@ -194,7 +195,7 @@ __device__ __forceinline__ void bwd_chunk(int t, int lane, int &r, int &c4, bool
 // +inf, so they contribute exactly 0.  On that (last) block the offsets are
 // recomputed from an opaque lane index, so that the compiler keeps no
 // second set live across the loop.
-template <int D, bool STATS>
+template <int D>
 __device__ __forceinline__ void bwd_fetch(const BwdBlock &k, int m0, float *__restrict__ qn,
                                           float *__restrict__ gn, float *__restrict__ stn)
 {
@@ -227,7 +228,7 @@ __device__ __forceinline__ void bwd_fetch(const BwdBlock &k, int m0, float *__re
             }
         }
     }
-    if (STATS && k.w == 0) {
+    if (k.w == 0) {
         const int lane = threadIdx.x & 63;
         if (lane < 16) dma16(lane < 8 ? k.l2p + m0 + 4 * lane : k.dlp + m0 + 4 * (lane - 8), stn);
     }
@@ -259,9 +260,9 @@ __device__ __forceinline__ DqState<D> dq_state(int w)
 }
 
 // The finished dQ block (rows m0..m0+31) to memory, by mode (kDqAtomic ...):
-// added into dq, stored into this wave's partial slab (dense rows of D
+// added into dq, or stored into this wave's partial slab (dense rows of D
 // floats, all 32 rows: the slab has S_pad rows; rows past S hold zeros and
-// are never read), or stored into dq.
+// are never read).
 template <int D, int DQ>
 __device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, int m0, const f32x16 &qacc)
 {
@@ -279,15 +280,6 @@ __device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, in
     // Row i of the block: wave-uniform row base + unsigned lane offset.
     float *dqb = k.dqp + (int64_t)m0 * k.in_ss + 32 * dblk;
     const unsigned qoff = (unsigned)(4 * h32 * k.in_ss + l32);
-    if constexpr (DQ == kDqDirect) {
-        static_assert(BwdLayout<D>::NSPLIT == 1, "direct dQ needs one wave per d block");
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float *rowp = dqb + (int64_t)(((i >> 2) * 8 + (i & 3)) * k.in_ss);
-            if (m0 + acc_row(i, h32) < k.S) rowp[qoff] = qacc[i] * a.scale;
-        }
-        return;
-    }
     if (m0 + kBq <= k.S) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -340,7 +332,7 @@ __device__ __forceinline__ void dq_softmax(const BwdArgs &a, const float *__rest
 //   3. the dQ product of block qb-1 (dS in LDS since the last barrier),
 //      interleaved with the softmax of block qb: its VALU work issues while
 //      the dQ MFMAs run, instead of leaving the matrix core idle;
-//   4. dQ of block qb-1 to memory (dq_store: atomics, partial or direct);
+//   4. dQ of block qb-1 to memory (dq_store: atomics or partial slab);
 //   5. dV += P^T dO, dK += dS^T Q of block qb;
 //   6. barrier (every wave has read dS of block qb-1; not needed with two
 //      dS buffers, see kDsBufs), dS of block qb to LDS, wait for the
@@ -374,7 +366,7 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
     const float *const ds = dsb + (parity ^ 1) * kDsStride;
     float *const ds_out = dsb + parity * kDsStride;
 
-    if (qb + 1 < k.nq) bwd_fetch<D, DQ != kDqDirect>(k, m0 + kBq, qn, gn, stn);
+    if (qb + 1 < k.nq) bwd_fetch<D>(k, m0 + kBq, qn, gn, stn);
 
     // ---- S, dP ----
     f32x16 sacc = zero16(), pacc = zero16();
@@ -481,10 +473,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     __shared__ float dOs0[L::QBUF], dOs1[L::QBUF];
     __shared__ float St0[2 * kBq], St1[2 * kBq];
     __shared__ float dSs[kDsBufs<D> * kBq * L::SSTR];
-    // kDqDirect: lse2 and delta of the (at most 4) query blocks, formed here;
-    // block qb's 32 lse2 values, then its 32 deltas, at 2 kBq * qb.
-    constexpr bool kSolo = DQ == kDqDirect;
-    __shared__ float SoloSt[kSolo ? 2 * kBk : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -508,12 +496,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
     k.qp = a.q + in_base;
     k.gp = a.dout + out_base;
-    if constexpr (!kSolo) {
-        k.l2p = a.lse2 + (int64_t)bh * a.S_pad;
-        k.dlp = a.delta + (int64_t)bh * a.S_pad;
-    } else {
-        k.l2p = k.dlp = nullptr;  // statistics live in SoloSt
-    }
+    k.l2p = a.lse2 + (int64_t)bh * a.S_pad;
+    k.dlp = a.delta + (int64_t)bh * a.S_pad;
     if constexpr (DQ == kDqPartial)
         k.dqp = a.dq_part + ((int64_t)(kb * L::NSPLIT + w / DB) * BH + bh) * a.S_pad * D;
     else
@@ -574,28 +558,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     // First block into buffer set 0; afterwards every step copies the next
     // block into the other set while it computes.
     const int qstart = CAUSAL ? n0 / kBq : 0;
-    bwd_fetch<D, !kSolo>(k, qstart * kBq, Qs0, dOs0, St0);
-    if constexpr (kSolo) {
-        // Row statistics of all S <= 128 rows: two threads per row, D/2
-        // floats of O and dO each.
-        const int r = tid >> 1, hf = tid & 1;
-        const int rr = r < S ? r : S - 1;
-        const float *__restrict__ orow = a.o + out_base + (int64_t)rr * a.out_ss + hf * (D / 2);
-        const float *__restrict__ grow = a.dout + out_base + (int64_t)rr * a.out_ss + hf * (D / 2);
-        float part = 0.0f;
-#pragma unroll
-        for (int c = 0; c < D / 2; c += 4) {
-            const f32x4 o4 = *(const f32x4 *)(orow + c);
-            const f32x4 g4 = *(const f32x4 *)(grow + c);
-            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
-        }
-        part += __shfl_xor(part, 1);
-        if (hf == 0) {
-            const int base = 2 * kBq * (r / kBq) + r % kBq;
-            SoloSt[base] = r < S ? a.lse[(int64_t)bh * S + r] * kLog2e : INFINITY;
-            SoloSt[base + kBq] = r < S ? part : 0.0f;
-        }
-    }
+    bwd_fetch<D>(k, qstart * kBq, Qs0, dOs0, St0);
     wait_vmem();
     __syncthreads();
 
@@ -604,29 +567,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     const int tail_bias = k.n0w + l32 >= S ? (1 << 24) : 0;
     auto walk = [&](auto mask) {
         constexpr bool M = decltype(mask)::value;
-        if constexpr (kSolo) {
-            // Statistics of block qb: its slice of SoloSt (nq <= 4; the
-            // next-block argument is unused, no statistics are copied).
-            auto stat = [&](int qb) { return SoloSt + 2 * kBq * (qb & 3); };
-            bwd_step<D, CAUSAL, false, M, DQ>(a, k, qstart, Qs0, dOs0, stat(qstart), dSs, 0, Qs1, dOs1,
-                                              St1, Kall, kr, vr, dvacc, dkacc, tail_bias);
-            for (int qb = qstart + 1; qb < k.nq; qb += 2) {
-                bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb, Qs1, dOs1, stat(qb), dSs, 1, Qs0, dOs0, St0,
+        bwd_step<D, CAUSAL, false, M, DQ>(a, k, qstart, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1, Kall, kr,
+                                          vr, dvacc, dkacc, tail_bias);
+        for (int qb = qstart + 1; qb < k.nq; qb += 2) {
+            bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb, Qs1, dOs1, St1, dSs, 1, Qs0, dOs0, St0, Kall, kr,
+                                             vr, dvacc, dkacc, tail_bias);
+            if (qb + 1 < k.nq)
+                bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb + 1, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1,
                                                  Kall, kr, vr, dvacc, dkacc, tail_bias);
-                if (qb + 1 < k.nq)
-                    bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb + 1, Qs0, dOs0, stat(qb + 1), dSs, 0, Qs1,
-                                                     dOs1, St1, Kall, kr, vr, dvacc, dkacc, tail_bias);
-            }
-        } else {
-            bwd_step<D, CAUSAL, false, M, DQ>(a, k, qstart, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1, Kall,
-                                              kr, vr, dvacc, dkacc, tail_bias);
-            for (int qb = qstart + 1; qb < k.nq; qb += 2) {
-                bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb, Qs1, dOs1, St1, dSs, 1, Qs0, dOs0, St0, Kall,
-                                                 kr, vr, dvacc, dkacc, tail_bias);
-                if (qb + 1 < k.nq)
-                    bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb + 1, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1,
-                                                     St1, Kall, kr, vr, dvacc, dkacc, tail_bias);
-            }
         }
     };
     if (CAUSAL || k.key_tail)
@@ -701,20 +649,12 @@ inline int64_t dq_part_floats(int64_t nkb, int64_t BH, int64_t S_pad)
     return nkb * BH * S_pad * (int64_t)kBk;
 }
 
-// Launches the backward for args: with no row statistics (args.lse2 null;
-// D = 128, S <= 128) the direct-dQ kernel alone; otherwise attn_bwd_pre and
-// the workgroup kernel, whose dQ is atomic or (args.dq_part set) partial,
-// then attn_bwd_dq_reduce.
+// Launches the backward for args: attn_bwd_pre and the workgroup kernel,
+// whose dQ is atomic or (args.dq_part set) partial, then
+// attn_bwd_dq_reduce.
 template <int D, bool CAUSAL>
 int launch_bwd(const BwdArgs &args, int64_t rows_pad, int nblocks)
 {
-    if constexpr (D == 128) {
-        if (!args.lse2) {
-            hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL, kDqDirect>), dim3(nblocks), dim3(kThreads), 0, 0,
-                               args);
-            return launch_ok("attn_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
-        }
-    }
     constexpr int RPB = 256 / (D / 4);
     const int pre_blocks = (int)((rows_pad + RPB - 1) / RPB);
     hipLaunchKernelGGL((attn_bwd_pre<D>), dim3(pre_blocks), dim3(256), 0, 0, args, rows_pad);

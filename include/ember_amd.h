@@ -74,9 +74,8 @@ void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak);
 
 /* Bitwise-reproducible results (no reference counterpart: the reference
  * has no operator whose result depends on timing).  Off by default.  The
- * only such operator here is attention_bwd's dq at S > 64 (see there for the
- * exception at D = 128); with
- * the switch on it is formed in a fixed order instead, at the cost of a
+ * only such operator here is attention_bwd's dq at S > 128 (S > 64 at
+ * D = 32); with the switch on it is formed in a fixed order instead, at the cost of a
  * scratch buffer and one extra pass.  Every other operator of this library
  * is reproducible either way.  The switch is process-wide; set it between
  * calls, not while another thread is inside the library. */
@@ -167,14 +166,14 @@ int attention_fwd(const float *q, const float *k, const float *v, float *o, floa
  * upstream gradient d_o, writes dq, dk, dv (same layout as q, k, v).  P is
  * recomputed from lse; the S x S matrix is never stored.  Needs
  * 2*B*H*S_pad*4 bytes of device scratch (S_pad = S rounded up to 32; none at
- * S <= 64, nor at S <= 128 with D = 128), which the library keeps cached
- * between calls.
- * Determinism: dk and dv are bitwise reproducible.  For S > 64, dq is
- * accumulated in HBM with fp32 atomic adds from every key block (128 keys)
- * that sees a query row, so its last bits vary from run to run (each run
- * within the stated tolerance).  At S <= 64, and at S <= 128 with D = 128
- * (one key block, whose waves each store a complete block of dq), dq is
- * stored once and reproducible too.  Because of the atomics dq must be
+ * S <= 64, nor at S <= 128 with D = 64 or 128), which the library keeps
+ * cached between calls.
+ * Determinism: dk and dv are bitwise reproducible.  For S > 128 (S > 64 at
+ * D = 32), dq is accumulated in HBM with fp32 atomic adds from every key
+ * block (128 keys) that sees a query row, so its last bits vary from run to
+ * run (each run within the stated tolerance).  At S <= 64, and at S <= 128
+ * with D = 64 or 128 (one workgroup per head, which forms each element of
+ * dq whole), dq is stored once and reproducible too.  Because of the atomics dq must be
  * device memory (not host or managed memory), and dq must not overlap q, k,
  * v, o, lse, d_o, dk or dv.
  * With ember_set_deterministic(1), the atomic cases instead store each key
@@ -196,15 +195,15 @@ int attention_bwd(const float *q, const float *k, const float *v, const float *o
  * array inside the library, one per GPU, held until the process ends, instead
  * of library-allocated scratch.  Limit: B*H*S_pad <= 2^21 rows (S_pad = S
  * rounded up to 32); a larger call returns EMBER_ERR_INVALID_ARGUMENT and
- * launches nothing (S <= 64, and S <= 128 at D = 128, need no statistics
- * and so no array space).
+ * launches nothing (S <= 64, and S <= 128 at D = 64 or 128, need no
+ * statistics and so no array space).
  * Every call on one GPU shares that GPU's array.  Calls
  * are ordered because all library work runs on the null stream; launches of
  * this entry point that overlap on one GPU (for example replayed on several
  * streams at once) race on the array.  Each call writes every statistic it
  * reads before reading it, so nothing carries over between calls.
  * With ember_set_deterministic(1), where attention_bwd would use the dq
- * partials (S > 64, except S <= 128 at D = 128) it returns
+ * partials (S > 128, or S > 64 at D = 32) it returns
  * EMBER_ERR_UNSUPPORTED and launches nothing: they need a buffer of the
  * problem's size. */
 int attention_bwd_noalloc(const float *q, const float *k, const float *v, const float *o,

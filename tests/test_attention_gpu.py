@@ -406,7 +406,7 @@ def test_peaked_scores_and_zero_scale(S, D, causal):
 
 
 @pytest.mark.parametrize("B,H,S,D,causal", [
-    (64, 64, 128, 128, True),    # direct-dQ workgroup kernel, 4096 heads
+    (64, 64, 128, 128, True),    # 16-key-chunk workgroup kernel, 4096 heads
     (32, 64, 130, 64, False),    # two key blocks, atomic dQ, 2048 heads
     (128, 64, 64, 128, True),    # persistent S <= 64 kernel, 8192 heads
     (256, 64, 32, 64, False),    # one-head LDS workgroups, 16384 heads

@@ -106,6 +106,26 @@ def test_short_backward_walks_many_heads(B, H, S, D, causal, pads, hpads):
     _run(300 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 
+@pytest.mark.parametrize("B,H,S,D,causal,pads,hpads", [
+    (2, 150, 128, 128, True, [0, 0], [0, 0]),
+    (3, 101, 128, 128, False, [4, 12], [1, 0]),
+    (1, 300, 113, 128, True, [0, 32], [3, 1]),
+    (4, 64, 65, 128, True, [12, 4], [0, 3]),
+    (2, 140, 96, 128, False, [0, 0], [0, 2]),
+    (2, 300, 128, 64, True, [0, 0], [0, 0]),
+    (5, 61, 127, 64, False, [4, 0], [1, 0]),
+    (1, 513, 80, 64, True, [32, 12], [0, 1]),
+    (3, 97, 65, 64, False, [0, 4], [3, 3]),
+    (2, 128, 100, 64, True, [12, 12], [1, 1]),
+])
+def test_s128_backward_many_heads(B, H, S, D, causal, pads, hpads):
+    """64 < S <= 128 at D = 64 and 128 (attn_bwd_s128: 16-key chunks dealt
+    out over the waves, the row statistics formed in the kernel, dQ stored
+    directly) with 256 to 600 heads, ragged S (one to eight 16-row chunks,
+    partial last chunks) and padded strides on both triples."""
+    _run(500 + B + H + S + D, B, H, S, D, causal, pads, hpads)
+
+
 def _run(seed, B, H, S, D, causal, pads, hpads):
     G.say(f"sweep seed={seed} B={B} H={H} S={S} D={D} causal={causal} pads={pads} hpads={hpads}")
     rng = np.random.default_rng(seed)

@@ -80,7 +80,7 @@ def test_attention_rejects_bad_layouts():
 
 def test_deterministic_switch_and_noalloc_refusal():
     """ember_set_deterministic is host state (no device call); with it on,
-    attention_bwd_noalloc refuses S > 64 (its dq partials would need a
+    attention_bwd_noalloc refuses S > 128 (its dq partials would need a
     buffer) before any device work, and still accepts the empty problem."""
     L = capi.lib()
     assert capi.is_deterministic() is False
@@ -89,7 +89,7 @@ def test_deterministic_switch_and_noalloc_refusal():
     try:
         capi.set_deterministic(True)
         assert L.ember_get_deterministic() == 1
-        assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 128, 64, 0.125, 1, *st, *st) == 2
+        assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 200, 64, 0.125, 1, *st, *st) == 2
         assert L.ember_get_last_error() == 2
         assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 0, 64, 0.125, 1, *st, *st) == 0
     finally:

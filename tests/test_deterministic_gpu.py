@@ -1,6 +1,6 @@
 """Deterministic mode (ember_set_deterministic) of attention_bwd on the GPU.
 
-With the switch on, S > 64 stores each key block's dQ contribution into a
+With the switch on, S > 128 stores each key block's dQ contribution into a
 partial slab and sums the slabs per row in ascending key order
 (attn_bwd_dq_reduce) instead of adding them into dQ with atomics.  Checked
 here, on contiguous and padded layouts, causal or not, every head dim, S
@@ -13,9 +13,9 @@ from 65 (one key block with a tail) to 4096 (32 key blocks):
   (max-abs 2e-4 / rel 1e-3), and padding stays untouched;
 * the Python front end (ember_amd.set_deterministic + attention_backward)
   takes the same path.
-S <= 64 has no atomics in either mode; one such case checks that the
-switch leaves it bitwise alone.  S <= 128 at D = 128 (the direct-dQ kernel,
-one store per element) is reproducible in both modes and is among the cases.
+S <= 64, and S <= 128 at D = 64 and 128 (attn_bwd_s128), have no atomics in
+either mode; one such case each checks that the switch leaves them bitwise
+alone.  S <= 128 at D = 32 takes the atomic kernel and is among the cases.
 """
 
 import numpy as np
@@ -80,7 +80,7 @@ CASES = [
     (2, 2, 129, 128, False, [12, 4], [0, 3]),
     (3, 5, 1000, 64, True, [0, 0], [0, 0]),
     (1, 1, 65, 32, False, [0, 0], [0, 0]),
-    (3, 3, 100, 128, True, [4, 0], [0, 1]),      # S <= 128 at D = 128: the direct-dQ kernel
+    (3, 3, 100, 128, True, [4, 0], [0, 1]),      # S <= 128 at D = 128: attn_bwd_s128, no atomics
     (2, 16, 1024, 64, True, [0, 0], [0, 0]),     # config 5's shape per head, 32 heads
 ]
 
@@ -113,9 +113,12 @@ def test_deterministic_dq_is_reproducible_and_exact(B, H, S, D, causal, pads, hp
         np.testing.assert_allclose(got[sl], ref, err_msg=name, **TOL)
 
 
-def test_deterministic_switch_leaves_short_sequences_alone(deterministic):
-    """S <= 64: the same kernels in both modes (no atomics there)."""
-    p = _Problem(4, 8, 48, 64, True, [4, 0], [1, 0], seed=7)
+@pytest.mark.parametrize("B,H,S,D,causal", [(4, 8, 48, 64, True), (2, 6, 112, 128, True),
+                                             (3, 5, 128, 64, False)])
+def test_deterministic_switch_leaves_short_sequences_alone(B, H, S, D, causal, deterministic):
+    """S <= 64, and S <= 128 at D = 64 or 128: the same kernels in both
+    modes (no atomics there)."""
+    p = _Problem(B, H, S, D, causal, [4, 0], [1, 0], seed=7 + S)
     (dq1, dk1, dv1), _ = p.backward()
     capi.set_deterministic(False)
     (dq0, dk0, dv0), _ = p.backward()
