@@ -15,7 +15,9 @@
 // instead, with no barriers (attn_fwd_wave, D = 128), or pack heads
 // (attn_fwd_packed, D <= 64): S <= 32 puts 4 heads in a workgroup (one per
 // wave, tiles of 32 keys) and S <= 64 puts 2 (two waves each), so that no
-// wave idles and every wave keeps loading.
+// wave idles and every wave keeps loading.  64 < S <= 96, and causal
+// S <= 128, at D >= 64 take attn_fwd_wave with one wave per pair of query
+// blocks.
 //
 // Per tile and wave (all products on v_mfma_f32_32x32x2f32):
 //   S^T (64 keys x 32 queries) = K_tile . Q^T   -- K from LDS, Q^T resident in
@@ -341,10 +343,13 @@ __global__ __launch_bounds__(kThreads, D == 64 ? 3 : 2) void attn_fwd_kernel(Fwd
     }
 }
 
-// D = 128, S <= 64: one wave per (head, 32-query block), four independent
+// D = 128 at S <= 64: one wave per (head, 32-query block), four independent
 // waves per workgroup (consecutive query blocks of a head share one) and no
 // barriers, so that two waves per SIMD overlap one's copies with another's
-// products in this HBM-bound regime.  Each wave stages its Q tile, then
+// products in this HBM-bound regime.  PAIR (64 < S <= 128, D >= 64; see
+// launch_fwd): one wave per pair of blocks p and nqb - 1 - p of a head,
+// taken one after the other, so that causally every wave has the same
+// number of key tiles.  Each wave stages its Q tile, then
 // each 32-key K tile, through a private padded LDS slice with coalesced
 // copies (buffer_load ... lds: an MFMA operand puts one row per lane, which
 // read straight from HBM would touch 64 lines per load), and loads V
@@ -359,7 +364,7 @@ struct WaveSlice {
     static constexpr int BUF = COP * 256;            // floats per wave slice
 };
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool PAIR>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
 {
     typedef WaveSlice<D> T;
@@ -373,18 +378,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
     const int l32 = lane & 31;
     float *__restrict__ buf = slab + w * T::BUF;
 
-    const int item = blockIdx.x * kWaves + w;  // query block fastest
-    if (item >= a.nbh * a.nqb) return;         // no barriers below: safe to leave
-    const int bh = item / a.nqb;
-    const int qb = item - bh * a.nqb;
+    // PAIR: a wave takes query blocks p and nqb - 1 - p of its head (p + 1
+    // and nqb - p key tiles causally: the same nqb + 1 for every wave);
+    // otherwise one block.
+    const int per_head = PAIR ? (a.nqb + 1) / 2 : a.nqb;
+    const int item = blockIdx.x * kWaves + w;  // query block (pair) fastest
+    if (item >= a.nbh * per_head) return;      // no barriers below: safe to leave
+    const int bh = item / per_head;
+    const int p0 = item - bh * per_head;
     const int b = bh / a.H;
     const int hh = bh - b * a.H;
     const int S = a.S;
-    const int m0 = 32 * qb;
-    const int mq = m0 + l32;
     const int in_ss = (int)a.in_ss;  // < 2^24 (checked on the host)
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const float *__restrict__ vb = a.v + in_base;
+    for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
+    const int qb = pass == 0 ? p0 : a.nqb - 1 - p0;
+    if (pass == 1 && qb == p0) break;  // odd nqb: the middle block alone
+    const int m0 = 32 * qb;
+    const int mq = m0 + l32;
 
     // Copies rows r0 .. r0+31 (clamped to S-1) of a (S, D) slab into buf;
     // copy t fills chunks 64t .. 64t+63, a padding or slack chunk re-reads
@@ -405,6 +417,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
     };
 
     // Q^T operand: lane holds Q[mq][h32*DH + kk] for k-step kk.
+    wait_lds();  // the previous block's reads of buf are complete
     stage(a.q + in_base, m0);
     wait_vmem();
     float qr[DH];
@@ -493,6 +506,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
             *(VT *)(orow + DB * r) = outv;
         }
         if (h32 == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
+    }
     }
 }
 
@@ -906,6 +920,22 @@ int launch_fwd(FwdArgs args, int64_t nbh)
                            0, 0, args);
         return launch_ok("attn_fwd_split") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
+    // 64 < S <= 96, and causal S <= 128 (D >= 64): one wave per pair of
+    // 32-query blocks.  The 128-query workgroups leave a quarter or more of
+    // their waves without rows at S <= 96, and causally their waves have 1
+    // to 4 key tiles (in lockstep) where a pair has the same 5.  Measured
+    // (B*H = 8192 heads at S = 80 and 96): +32-36 % causal, +15-17 %
+    // non-causal; causal S = 112 and 128: +3 % and equal; non-causal
+    // S = 128: -14 to -22 %, so that case stays with the workgroups.
+    if constexpr (D >= 64) {
+        if (args.S > 64 && (args.S <= 96 || (CAUSAL && args.S <= 128))) {
+            args.nqb = (args.S + 31) / 32;
+            const int64_t items = (int64_t)(args.nqb + 1) / 2 * nbh;
+            hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, true>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
+                               dim3(kThreads), 0, 0, args);
+            return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
+        }
+    }
     if (args.S > 64) {
         args.nqb = (args.S + kBr - 1) / kBr;
         const int nblocks = args.nqb * (int)nbh;
@@ -918,7 +948,7 @@ int launch_fwd(FwdArgs args, int64_t nbh)
         // kernel is as fast or faster.
         args.nqb = (args.S + 31) / 32;
         const int64_t items = (int64_t)args.nqb * nbh;
-        hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
+        hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, false>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
                            dim3(kThreads), 0, 0, args);
         return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
     } else {
