@@ -392,9 +392,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
     const int in_ss = (int)a.in_ss;  // < 2^24 (checked on the host)
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const float *__restrict__ vb = a.v + in_base;
-    for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
-    const int qb = pass == 0 ? p0 : a.nqb - 1 - p0;
-    if (pass == 1 && qb == p0) break;  // odd nqb: the middle block alone
+    // Query block qb of head bh.
+    auto block = [&](int qb) {
     const int m0 = 32 * qb;
     const int mq = m0 + l32;
 
@@ -417,7 +416,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
     };
 
     // Q^T operand: lane holds Q[mq][h32*DH + kk] for k-step kk.
-    wait_lds();  // the previous block's reads of buf are complete
     stage(a.q + in_base, m0);
     wait_vmem();
     float qr[DH];
@@ -507,6 +505,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
         }
         if (h32 == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
     }
+    };
+    block(p0);
+    if constexpr (PAIR) {
+        if (a.nqb - 1 - p0 != p0) {  // odd nqb: the middle block alone
+            wait_lds();  // the first block's reads of buf are complete
+            block(a.nqb - 1 - p0);
+        }
     }
 }
 
