@@ -274,8 +274,8 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
     # The backward in the same regime: algorithmic bytes 32*B*H*S*D + 8*B*H*S
     # (read q, k, v, o, dO, lse; write dq, dk, dv).  S <= 64: LDS-staged
     # workgroups (one per head at S <= 32, persistent with a register
-    # prefetch of the next head at S = 64); S = 128: the key-block workgroup
-    # kernel.
+    # prefetch of the next head at S = 64); S = 128: attn_bwd_s128 (one
+    # workgroup per head, 16-key chunks dealt out evenly over the waves).
     for S, D in ((32, 64), (32, 128), (64, 64), (64, 128), (128, 64), (128, 128)):
         B, H = (1 << 20) // S // 64, 64
         n = B * H * S * D
@@ -397,8 +397,8 @@ def secondary(L, ev):
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)
         attn(f"short_s{S}_fwd", (1 << 20) // S // 64, 64, S, 128, True, False, 20)
     # The backward where it is HBM-bound (AI = S/8 causal): S = 32 and 64
-    # (one LDS-staged workgroup per head) and S = 128 (the key-block
-    # workgroup kernel).
+    # (one LDS-staged workgroup per head) and S = 128 (attn_bwd_s128, at the
+    # ridge point: one workgroup per head, 16-key chunks dealt out evenly).
     for S in (32, 64, 128):
         for D in (64, 128):
             attn(f"short_s{S}_d{D}_fwd_bwd", (1 << 20) // S // 64, 64, S, D, True, True, 20)
