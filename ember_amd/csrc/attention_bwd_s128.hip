@@ -18,24 +18,27 @@
 // One workgroup per head; wave w keeps K and V of its key chunks resident in
 // registers (B operands of S = Q K^T and dP = dO V^T) and accumulates dK, dV
 // for them in registers:
-//   D = 128: 8 waves, one chunk each; waves w and w + 4 share a SIMD and
-//     hold chunks w and 7 - w (2 waves per SIMD, one workgroup per CU,
-//     136 KB of LDS);
-//   D = 64: 4 waves, chunks w and 7 - w each (76 KB of LDS, two workgroups
+//   D = 128: 8 waves, one chunk each, chunks w and 7 - w on waves w and
+//     w + 4 (the hardware's round-robin placement puts those on one SIMD;
+//     2 waves per SIMD, 137 KB of LDS, one workgroup per CU), persistent
+//     (below);
+//   D = 64: 4 waves, chunks w and 7 - w each (80 KB of LDS, two workgroups
 //     per CU, which also overlap one head's loads with another's products).
 // The workgroup walks 16-query chunks qc in lockstep, with the next chunk's
-// Q, dO and O rows copied HBM -> LDS (global_load_lds_dwordx4, no registers)
-// into the second of two buffers while the current one is multiplied:
+// Q, dO and O rows copied HBM -> LDS (buffer_load ... lds, no registers)
+// into the second of two buffers while the current one is multiplied.
+// Step qc:
+//   dQ of chunk qc - 1 = scale * dS . K over all keys at or before it, one
+//     16-column block per wave, dS and K^T from LDS; stored straight to dq in
+//     the next step (every element written once: no atomics, no scratch,
+//     reproducible);
 //   S, dP of each active (key chunk, qc) pair; delta = <dO, O> of the 16
 //     rows, formed by every wave from the LDS rows (no separate pass, no
 //     extra barrier); P = exp2(S*c - lse2), dS = P * (dP - delta), masked at
 //     the diagonal and past S;
-//   dV += P^T dO, dK += dS^T Q (the P / dS accumulators are the A operands
-//     directly); dS to LDS;
-//   barrier; dQ of chunk qc = scale * dS . K over all keys at or before it,
-//     one 16-column block per wave, K read transposed from LDS; stored
-//     straight to dq (every element written once: no atomics, no scratch,
-//     reproducible).
+//   dS to LDS; dV += P^T dO, dK += dS^T Q (the P / dS accumulators are the
+//     A operands directly);
+//   barrier.
 // lse2 of all rows is formed once per head into LDS (rows past S: +inf, so
 // their P is exactly 0; their Q, dO, O rows re-read row S-1).
 #include "attention_bwd_kernels.h"

@@ -101,6 +101,13 @@ def test_noalloc_matches_attention_bwd_on_consecutive_calls():
     new = short.compare()
     assert np.array_equal(new[0], short.out["attention_bwd"][0].numpy())
 
+    # 4) 64 < S <= 128 at D = 128: one workgroup per head, no statistics, no atomics
+    mid128 = _Case(3, 4, 100, 128, True, 5)
+    capi.check(mid128.run("attention_bwd_noalloc"), "attention_bwd_noalloc")
+    capi.check(mid128.run("attention_bwd"), "attention_bwd")
+    new = mid128.compare()
+    assert np.array_equal(new[0], mid128.out["attention_bwd"][0].numpy())
+
 
 def test_noalloc_rejects_more_rows_than_its_array():
     """B*H*S_pad = 2^21 + 32 rows: EMBER_ERR_INVALID_ARGUMENT, nothing launched
