@@ -12,12 +12,12 @@
 // products: V of tile t lands while S of tile t is computed, K of tile t+1
 // while V of tile t is multiplied; two barriers per tile.
 // Short sequences (S <= 64, HBM-bound) use one wave per 32-query block
-// instead, with no barriers (attn_fwd_wave, D = 128), or pack heads
-// (attn_fwd_packed, D <= 64): S <= 32 puts 4 heads in a workgroup (one per
-// wave, tiles of 32 keys) and S <= 64 puts 2 (two waves each), so that no
-// wave idles and every wave keeps loading.  64 < S <= 96, and causal
-// S <= 128, at D >= 64 take attn_fwd_wave with one wave per pair of query
-// blocks.
+// instead, with no barriers (attn_fwd_wave, D >= 64), or pack heads
+// (attn_fwd_packed: D = 32, and non-causal D = 64 at S > 32): S <= 32 puts
+// 4 heads in a workgroup (one per wave, tiles of 32 keys) and S <= 64 puts
+// 2 (two waves each), so that no wave idles and every wave keeps loading.
+// 64 < S <= 96, and causal S <= 128, at D >= 64 take attn_fwd_wave with one
+// wave per pair of query blocks.
 //
 // Per tile and wave (all products on v_mfma_f32_32x32x2f32):
 //   S^T (64 keys x 32 queries) = K_tile . Q^T   -- K from LDS, Q^T resident in
@@ -343,7 +343,8 @@ __global__ __launch_bounds__(kThreads, D == 64 ? 3 : 2) void attn_fwd_kernel(Fwd
     }
 }
 
-// D = 128 at S <= 64: one wave per (head, 32-query block), four independent
+// S <= 64 (D = 128; D = 64 but non-causal S > 32, see launch_fwd): one
+// wave per (head, 32-query block), four independent
 // waves per workgroup (consecutive query blocks of a head share one) and no
 // barriers, so that two waves per SIMD overlap one's copies with another's
 // products in this HBM-bound regime.  PAIR (64 < S <= 128, D >= 64; see
@@ -947,16 +948,22 @@ int launch_fwd(FwdArgs args, int64_t nbh)
         hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL>), dim3(nblocks), dim3(kThreads), 0, 0, args);
         return launch_ok("attn_fwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
-    if constexpr (D == 128) {
-        // Measured: the wave kernel moves 4.7 (S = 32) and 4.0 TB/s (S = 64)
-        // where the packed kernel moves 3.8 and 2.9; at D <= 64 the packed
-        // kernel is as fast or faster.
-        args.nqb = (args.S + 31) / 32;
-        const int64_t items = (int64_t)args.nqb * nbh;
-        hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, false>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
-                           dim3(kThreads), 0, 0, args);
-        return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
-    } else {
+    // S <= 64: the wave kernel at D = 128 (4.7 TB/s at S = 32 and 4.0 at
+    // S = 64, where the packed kernel moves 3.8 and 2.9) and at D = 64
+    // (causal +9-13 % at S = 32, +25 % at S = 48, +5-11 % at S = 64,
+    // non-causal +6 % at S = 32; 8192-32768 heads), except non-causal
+    // D = 64 at 32 < S <= 64 (-1.5 %) and D = 32, which keep the packed
+    // kernel.
+    if constexpr (D >= 64) {
+        if (D == 128 || CAUSAL || args.S <= 32) {
+            args.nqb = (args.S + 31) / 32;
+            const int64_t items = (int64_t)args.nqb * nbh;
+            hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, false>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
+                               dim3(kThreads), 0, 0, args);
+            return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
+        }
+    }
+    if constexpr (D < 128) {
         args.nqb = 1;
         if (args.S <= 32)
             hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 4, 32>), dim3((unsigned)((nbh + 3) / 4)),
@@ -966,6 +973,7 @@ int launch_fwd(FwdArgs args, int64_t nbh)
                                dim3(kThreads), 0, 0, args);
         return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
+    return EMBER_OK;  // not reached: D = 128 always takes the wave kernel above
 }
 
 }  // namespace
