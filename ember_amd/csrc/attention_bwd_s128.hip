@@ -438,9 +438,12 @@ __global__ __launch_bounds__(S128Shape<D>::NW * 64, D == 128 ? 1 : 2) void attn_
 template <int D, bool CAUSAL>
 int launch_s128(const BwdArgs &args, int nbh)
 {
-    int ncu = device_cu_count();
-    if (ncu <= 0) return record_error(EMBER_ERR_DEVICE, "hipDeviceGetAttribute(CU count)");
-    const int grid = !S128Shape<D>::PERSIST || nbh < ncu ? nbh : ncu;
+    int grid = nbh;  // one workgroup per head, or (persistent) one per CU
+    if constexpr (S128Shape<D>::PERSIST) {
+        const int ncu = device_cu_count();
+        if (ncu <= 0) return record_error(EMBER_ERR_DEVICE, "hipDeviceGetAttribute(CU count)");
+        if (ncu < nbh) grid = ncu;
+    }
     hipLaunchKernelGGL((attn_bwd_s128<D, CAUSAL>), dim3((unsigned)grid), dim3(S128Shape<D>::NW * 64), 0, 0,
                        args, nbh);
     return launch_ok("attn_bwd_s128") ? EMBER_OK : EMBER_ERR_DEVICE;
