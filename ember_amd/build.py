@@ -38,6 +38,7 @@ HIP_SOURCES = [
     ("attention_bwd.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]),
     ("attention_bwd_c128.hip", []),
     ("attention_bwd_s128.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]),
+    ("attention_bwd_w16.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]),
     ("optim.hip", []),
     ("layernorm.hip", []),
     ("block_ops.hip", []),

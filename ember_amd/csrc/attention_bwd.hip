@@ -835,11 +835,12 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.out_sh = out_sh;
     args.out_ss = out_ss;
     const int nblocks = args.nkb * (int)(B * H);
+    // D = 64: 16-key chunks, three workgroups per CU (attention_bwd_w16.hip);
+    // D = 32 and 128: the key-block workgroup kernel.
+    if (D == 64) return launch_bwd_w16(args, rows_pad, causal != 0, (int)(B * H));
     switch (D * 2 + (causal ? 1 : 0)) {
         case 64: return launch_bwd<32, false>(args, rows_pad, nblocks);
         case 65: return launch_bwd<32, true>(args, rows_pad, nblocks);
-        case 128: return launch_bwd<64, false>(args, rows_pad, nblocks);
-        case 129: return launch_bwd<64, true>(args, rows_pad, nblocks);
         case 256: return launch_bwd<128, false>(args, rows_pad, nblocks);
         default: return launch_bwd_causal_d128(args, rows_pad, nblocks);
     }

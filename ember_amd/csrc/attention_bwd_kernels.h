@@ -83,6 +83,9 @@ int launch_bwd_causal_d128(const BwdArgs &args, int64_t rows_pad, int nblocks);
 // per head (no row statistics or dq partials: args.lse2, delta, dq_part
 // unused).
 int launch_bwd_s128(const BwdArgs &args, int D, bool causal, int nbh);
+// attention_bwd_w16.hip: D = 64 at S > 128 (attn_bwd_pre, attn_bwd_w16 and,
+// when args.dq_part is set, attn_bwd_dq_reduce).
+int launch_bwd_w16(const BwdArgs &args, int64_t rows_pad, bool causal, int nbh);
 
 namespace {
 
@@ -609,15 +612,16 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
 }
 
 // Deterministic mode's second pass: dq[b, h, m, :] = the sum of the partial
-// slabs in ascending key order (slab j holds keys 128/NSPLIT * j onwards;
-// causal: only the slabs of the key blocks at or before row m, the ones the
-// main kernel wrote for it), one thread per 4 floats.  The order is fixed,
-// so dq is bitwise reproducible.
+// slabs in ascending key order (slab j holds keys KPS * j .. KPS * j + KPS - 1,
+// KPS = 128/NSPLIT; causal: only the slabs that start at or before row m,
+// every one of which the main kernel wrote for that row; non-causal: the
+// slabs that start inside the sequence), one thread per 4 floats.  The order
+// is fixed, so dq is bitwise reproducible.
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dq_reduce(BwdArgs a, int BH)
 {
     constexpr int TPR = D / 4;
-    constexpr int NSPLIT = BwdLayout<D>::NSPLIT;
+    constexpr int KPS = kBk / BwdLayout<D>::NSPLIT;  // keys per slab
     const int64_t slab = (int64_t)BH * a.S_pad * D;  // floats per slab
     const int64_t n = (int64_t)BH * a.S * TPR;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
@@ -626,7 +630,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_reduce(BwdArgs a, int BH)
         const int64_t row = idx / TPR;
         const int bh = (int)(row / a.S);
         const int m = (int)(row - (int64_t)bh * a.S);
-        const int nslab = (CAUSAL ? m / kBk + 1 : a.nkb) * NSPLIT;
+        const int nslab = CAUSAL ? m / KPS + 1 : (a.S + KPS - 1) / KPS;
         const float *p = a.dq_part + ((int64_t)bh * a.S_pad + m) * D + 4 * sub;
         f32x4 acc = *(const f32x4 *)p;
         for (int j = 1; j < nslab; ++j) {
