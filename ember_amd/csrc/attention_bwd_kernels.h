@@ -160,7 +160,9 @@ constexpr int kDqAtomic = 0, kDqPartial = 1;
 
 // Buffers for a block's dS: two at D = 64, used by alternate blocks, which
 // saves one barrier per block (bwd_step; +2-3 % at D = 64); one at D = 128
-// (no LDS left) and at D = 32 (two measured -1 to -4 % causal).
+// (no LDS left) and at D = 32 (two measured -1 to -4 % causal).  The
+// library instantiates this kernel at D = 32 and 128; D = 64 runs
+// attn_bwd_w16 (attention_bwd_w16.hip), which measured faster there.
 template <int D>
 constexpr int kDsBufs = D == 64 ? 2 : 1;
 
