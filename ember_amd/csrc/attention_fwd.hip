@@ -988,6 +988,10 @@ int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t 
     if (D != 32 && D != 64 && D != 128) return record_error(EMBER_ERR_UNSUPPORTED, who);
     if (S > (int64_t)INT32_MAX / 2 || B * H > (int64_t)INT32_MAX / 1024)
         return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
+    // At most 2^33 elements (32 GiB) per tensor: the backward's nine tensors
+    // then fill an MI355X's 288 GB, and every launch's grid stays below 2^32
+    // work-items (the largest, attn_bwd_pre, runs D/4 per padded row).
+    if (B * H * S * D > (int64_t(1) << 33)) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     for (int i = 0; i < nstrides; ++i)
         if (strides[i] < 0 || (strides[i] & 3)) return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     // Row strides (the third of each triple) index rows with 32-bit offsets.

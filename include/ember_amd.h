@@ -147,8 +147,9 @@ int softmax_axis(const float *a, float *out, int outer, int inner, int axis_dim)
  * and of o (and d_o) at b*out_sb + h*out_sh + s*out_ss + d, so packed
  * (B, S, 3, H, D) projections are read and (B, S, H, D) outputs written
  * without copies.  d must be contiguous, every stride a multiple of 4, the
- * row strides (in_ss, out_ss) below 2^24, every pointer 16-byte aligned and
- * scale finite and >= 0.  lse is dense (B, H, S), natural log.
+ * row strides (in_ss, out_ss) below 2^24, B*H*S*D at most 2^33, every
+ * pointer 16-byte aligned and scale finite and >= 0.  lse is dense
+ * (B, H, S), natural log.
  *
  * Semantics (the CPU restatement in oracle/ember_oracle.c is the checker):
  *   s[i][j] = scale * <q_i, k_j>;  key j visible to query i iff j <= i when

@@ -74,6 +74,9 @@ def test_attention_rejects_bad_layouts():
     assert _fwd_call(ptr=18) == 1                      # not 16-byte aligned
     assert _fwd_call(strides=(512, 512, 66)) == 1      # stride not a multiple of 4
     assert _fwd_call(B=-1) == 1
+    # More than 2^33 elements per tensor (B*H*S*D = 2^34): rejected before any
+    # device work, so that no launch's grid can pass 2^32 work-items.
+    assert _fwd_call(B=1, H=1 << 10, S=1 << 17, D=128) == 1
     L.ember_get_last_error()
     assert _fwd_call(S=0) == 0                         # empty: nothing to do
 
