@@ -11,10 +11,11 @@
 // issue) idles the matrix core, and causally each workgroup computes 128 x
 // 128 diagonal scores of which half are masked.  Here a workgroup holds 64
 // keys, one 16-key chunk per wave on v_mfma_f32_16x16x4f32 (the same rate per
-// flop): K, V, dK, dV of a chunk take 4 x 16 registers per lane, and the LDS
-// holds two 16-query chunk sets, the dS of two chunks and K^T of the 64 keys
-// (46 KB), so three independent workgroups share a CU and fill each other's
-// waits, and masked work is cut at 16 x 16.  At D = 128 the same design
+// flop): K, V, dK, dV of a chunk take 4 x 16 registers per lane (126 in
+// all), and the LDS holds two 16-query chunk sets, the dS of one chunk and
+// K^T of the 64 keys (39 KB), so four independent workgroups share a CU and
+// fill each other's waits, and masked work is cut at 16 x 16.  (Three per CU
+// with a second dS buffer and one barrier per step measured 3-6 % slower.)  At D = 128 the same design
 // (188 registers, 79 KB, two workgroups per CU) measured 5-7 % slower than
 // the key-block kernel, which keeps that case.
 //
@@ -24,11 +25,12 @@
 //     LDS into the other set;
 //   dQ of chunk qc - 1 = dS . K over the workgroup's keys at or before it,
 //     D/4 columns per wave, dS and K^T from LDS;
+//   barrier (every wave has read dS of chunk qc - 1);
 //   S, dP of this wave's (key chunk, qc) pair when active; P = exp2(S*c -
 //     lse2), dS = P * (dP - delta), masked at the diagonal and past S; dS to
 //     LDS; dV += P^T dO, dK += dS^T Q with the P / dS accumulators as the A
 //     operands;
-//   one barrier.
+//   barrier.
 // dQ goes out with atomics, or (deterministic mode) into slab kb of the
 // partials, which attn_bwd_dq_reduce sums in key order: the workgroup's 64
 // keys are exactly the 64 keys of that slab at D = 64, and it writes the slab
@@ -46,7 +48,7 @@ struct W16Shape {
     static constexpr int STR = D + 4;                     // padded row of a chunk tile
     static constexpr int ROWCH = STR / 4;                 // 16-byte pieces per padded row
     static constexpr int TCOP = (16 * ROWCH + 63) / 64;   // 1 KiB copies per 16-row tile
-    static constexpr int TILE = TCOP * 256;               // floats per tile
+    static constexpr int TILE = 16 * STR;                 // floats per tile (a copy's lanes past it are masked)
     static constexpr int SET = 2 * TILE + 32;             // Q and dO tiles, then lse2 and delta of 16 rows
     static constexpr int SL = (TCOP + 1) / 2;             // copies per wave (two waves per tile)
     static constexpr int XSTR = KB + 4;                   // padded row of dS (16 x KB) and K^T (D x KB)
@@ -68,13 +70,13 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c)
 //     dO[4g + r][64h + 4n + j] as the B operand of column block 4h + j;
 //   dQ = dS K: lane (n, g) reads dS[n][16c + 4g + j] and K^T[d][16c + 4g + j].
 template <int D, bool CAUSAL, int DQ>
-__global__ __launch_bounds__(256, D == 128 ? 2 : 3) void attn_bwd_w16(BwdArgs a, int nkb)
+__global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
 {
     typedef W16Shape<D> L;
     constexpr int NW = L::NW, DH = L::DH, STR = L::STR, XSTR = L::XSTR, NH = L::NH, NB = L::NB,
                   QB = L::QB, CPW = L::KB / 16;
     __shared__ float sets[2 * L::SET];    // two chunk sets
-    __shared__ float dsb[2 * 16 * XSTR];  // dS of a query chunk, alternate chunks alternate halves
+    __shared__ float dsb[16 * XSTR];      // dS of a query chunk
     __shared__ float Kt[D * XSTR];        // K^T of the workgroup's keys
 
     const int lane = threadIdx.x & 63;
@@ -146,7 +148,8 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void attn_bwd_w16(BwdArgs a,
 #pragma unroll
         for (int sl = 0; sl < L::SL; ++sl) {
             const int u = (w & 1) + 2 * sl;
-            if (u < L::TCOP) dma16_buf(rsrc, full ? coff[sl] : piece(u, ln, S - 1 - m0), tdst + 256 * u);
+            if (u < L::TCOP && 64 * u + lane < 16 * L::ROWCH)
+                dma16_buf(rsrc, full ? coff[sl] : piece(u, ln, S - 1 - m0), tdst + 256 * u);
         }
         if (w == 0 && lane < 8) dma16(lane < 4 ? l2p + m0 + 4 * lane : dlp + m0 + 4 * (lane - 4), dst + 2 * L::TILE);
     };
@@ -265,15 +268,16 @@ __global__ __launch_bounds__(256, D == 128 ? 2 : 3) void attn_bwd_w16(BwdArgs a,
         const int st = (qc - qstart) & 1;
         if (qc >= qstart + 2) store_dq(qc - 2, qa);
         if (qc + 1 < nch) fetch(qc + 1, sets + (st ^ 1) * L::SET);
-        if (qc >= qstart + 1) dq_product(qc - 1, dsb + (st ^ 1) * 16 * XSTR, qa);
-        if (kvalid && (!CAUSAL || kc <= qc)) products(qc, sets + st * L::SET, dsb + st * 16 * XSTR);
+        if (qc >= qstart + 1) dq_product(qc - 1, dsb, qa);
+        __syncthreads();  // every wave has read dS of chunk qc - 1
+        if (kvalid && (!CAUSAL || kc <= qc)) products(qc, sets + st * L::SET, dsb);
         wait_vmem();      // this wave's copies of chunk qc + 1 have landed
         __syncthreads();  // dS of chunk qc and all of chunk qc + 1 in LDS
     }
     if (nch - qstart >= 2) store_dq(nch - 2, qa);
     {
         f32x4 ql[QB];
-        dq_product(nch - 1, dsb + ((nch - 1 - qstart) & 1) * 16 * XSTR, ql);
+        dq_product(nch - 1, dsb, ql);
         store_dq(nch - 1, ql);
     }
 
