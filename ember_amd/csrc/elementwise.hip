@@ -21,6 +21,8 @@
 #include <math.h>
 
 #include "common.h"
+#include "lds_dma.h"
+#include "mfma.h"
 
 namespace ember {
 namespace {
@@ -267,6 +269,101 @@ __global__ __launch_bounds__(64) void k_reduce_rows(const float *a, float *out, 
     if (lane < nr) out[r0 + lane] = acc;
 }
 
+// The same fold with the loads pipelined (L % 4 == 0, L < 2^24, a 16-byte
+// aligned): a one-wave workgroup owns 64 rows; each 64-column chunk is copied
+// HBM -> LDS by direct 16-byte copies (buffer form: the chunk's base in a
+// scalar descriptor, a fixed 32-bit byte offset per lane and copy) into rows
+// padded to 68 floats, kRing chunks in flight (17 copies each; vmcnt counts
+// at most 63).  A piece past the row (the 17th) or past the matrix re-reads
+// the chunk's first piece: valid memory, never folded.  Lane r folds row r in
+// index order from 128-bit LDS reads (conflict-free: 8 consecutive rows start
+// 16 bytes apart in the 128-byte bank cycle), all 16 reads of a chunk before
+// its adds.  One wave, so no barriers: a chunk is consumed after this wave's
+// own vmcnt wait and refilled after its fold has read it.
+constexpr int kRowStr = 68;                 // floats per padded tile row
+constexpr int kTileCopies = 64 * 17 / 64;   // 1 KiB copies per 64 x 64 tile
+constexpr int kRing = 4;                    // chunks in flight
+
+template <bool MAX>
+__global__ __launch_bounds__(64) void k_reduce_rows_ring(const float *a, float *out, int rows, int L)
+{
+    using ember::f32x4;
+    __shared__ float tile[kRing * 64 * kRowStr];
+    const int lane = threadIdx.x;
+    const int r0 = blockIdx.x * 64;
+    const int nr = min(64, rows - r0);
+    const int nchunk = (L + 63) / 64;
+    const float *row0 = a + (int64_t)r0 * L;
+    // Byte offset of this lane's piece in copy t of a chunk whose columns
+    // from cend on lie past the row (0: the chunk's first piece).
+    auto offset = [&](int t, int ln, int cend) {
+        const int p = 64 * t + ln;
+        const int r = p / 17, q = p - 17 * r;
+        return q < 16 && r < nr && 4 * q < cend ? 4u * (unsigned)(r * L + 4 * q) : 0u;
+    };
+    unsigned off[kTileCopies];
+#pragma unroll
+    for (int t = 0; t < kTileCopies; ++t) off[t] = offset(t, lane, 64);
+    auto issue = [&](int ch) {
+        float *dst = tile + (ch % kRing) * 64 * kRowStr;
+        const __amdgpu_buffer_rsrc_t rs = ember::dma_rsrc(row0 + 64 * ch);
+        const int cend = L - 64 * ch;
+        if (cend >= 64) {
+#pragma unroll
+            for (int t = 0; t < kTileCopies; ++t) ember::dma16_buf(rs, off[t], dst + 256 * t);
+        } else {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));  // the tail's offsets: recomputed, not kept live
+#pragma unroll
+            for (int t = 0; t < kTileCopies; ++t) ember::dma16_buf(rs, offset(t, ln, cend), dst + 256 * t);
+        }
+    };
+    for (int ch = 0; ch < min(kRing, nchunk); ++ch) issue(ch);
+    float acc = 0.0f;
+    for (int ch = 0; ch < nchunk; ++ch) {
+        // Chunks ch + 1 .. issued after this one may stay in flight.
+        switch (min(kRing - 1, nchunk - 1 - ch)) {
+            case 3: ember::wait_vmem_n<3 * kTileCopies>(); break;
+            case 2: ember::wait_vmem_n<2 * kTileCopies>(); break;
+            case 1: ember::wait_vmem_n<kTileCopies>(); break;
+            default: ember::wait_vmem(); break;
+        }
+        if (lane < nr) {
+            const float *t = tile + (ch % kRing) * 64 * kRowStr + lane * kRowStr;
+            const int nc = min(64, L - 64 * ch);
+            if (nc == 64) {
+                f32x4 v[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) v[q] = *(const f32x4 *)(t + 4 * q);
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (MAX)
+                            acc = (ch == 0 && q == 0 && j == 0) ? v[q][j] : fmaxf(acc, v[q][j]);
+                        else
+                            acc += v[q][j];
+                    }
+            } else {
+                for (int j0 = 0; j0 < nc; j0 += 4) {
+                    const f32x4 v = *(const f32x4 *)(t + j0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (j0 + j < nc) {
+                            if (MAX)
+                                acc = (ch == 0 && j0 + j == 0) ? v[j] : fmaxf(acc, v[j]);
+                            else
+                                acc += v[j];
+                        }
+                    }
+                }
+            }
+        }
+        if (ch + kRing < nchunk) issue(ch + kRing);
+    }
+    if (lane < nr) out[r0 + lane] = acc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -326,8 +423,12 @@ void sum_axis(const float *a, float *out, int outer_stride, int inner_stride, in
     const int total = outer_stride * inner_stride;
     if (total <= 0) return;
     if (inner_stride == 1 && axis_dim > 1) {
-        hipLaunchKernelGGL(k_reduce_rows<false>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
-                           out, outer_stride, axis_dim);
+        if (axis_dim % 4 == 0 && axis_dim < (1 << 24) && ((uintptr_t)a & 15) == 0)
+            hipLaunchKernelGGL(k_reduce_rows_ring<false>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
+                               out, outer_stride, axis_dim);
+        else
+            hipLaunchKernelGGL(k_reduce_rows<false>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
+                               out, outer_stride, axis_dim);
         ember::launch_ok("sum_axis");
         return;
     }
@@ -341,8 +442,12 @@ void max_axis(const float *a, float *out, int outer_stride, int inner_stride, in
     const int total = outer_stride * inner_stride;
     if (total <= 0 || axis_dim <= 0) return;
     if (inner_stride == 1 && axis_dim > 1) {
-        hipLaunchKernelGGL(k_reduce_rows<true>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
-                           out, outer_stride, axis_dim);
+        if (axis_dim % 4 == 0 && axis_dim < (1 << 24) && ((uintptr_t)a & 15) == 0)
+            hipLaunchKernelGGL(k_reduce_rows_ring<true>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
+                               out, outer_stride, axis_dim);
+        else
+            hipLaunchKernelGGL(k_reduce_rows<true>, dim3((outer_stride + 63) / 64), dim3(64), 0, 0, a,
+                               out, outer_stride, axis_dim);
         ember::launch_ok("max_axis");
         return;
     }
