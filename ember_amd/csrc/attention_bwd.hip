@@ -1,7 +1,9 @@
 // attention_bwd.hip -- entry point of the fused flash-attention backward
-// (fp32, gfx950); the workgroup kernels (S > 64) are in
-// attention_bwd_kernels.h, the short-sequence kernels (S <= 64: one
-// workgroup per head with Q, K, V, dO staged in LDS) are below.
+// (fp32, gfx950); the short-sequence kernels (S <= 64: one workgroup per head
+// with Q, K, V, dO staged in LDS) are below; 64 < S <= 128 at D = 64 and 128
+// runs attn_bwd_s128 (attention_bwd_s128.hip), longer D = 64 attn_bwd_w16
+// (attention_bwd_w16.hip), and the rest the key-block workgroup kernel of
+// attention_bwd_kernels.h.
 //
 // No reference counterpart (pawel002/ember has no attention): the operator is
 // new, slotted beside matmul in src/tensor/operators.h:20-27.  Its semantics
@@ -835,7 +837,7 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.out_sh = out_sh;
     args.out_ss = out_ss;
     const int nblocks = args.nkb * (int)(B * H);
-    // D = 64: 16-key chunks, three workgroups per CU (attention_bwd_w16.hip);
+    // D = 64: 16-key chunks, four workgroups per CU (attention_bwd_w16.hip);
     // D = 32 and 128: the key-block workgroup kernel.
     if (D == 64) return launch_bwd_w16(args, rows_pad, causal != 0, (int)(B * H));
     switch (D * 2 + (causal ? 1 : 0)) {
