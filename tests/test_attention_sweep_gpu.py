@@ -126,6 +126,24 @@ def test_s128_backward_many_heads(B, H, S, D, causal, pads, hpads):
     _run(500 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 
+@pytest.mark.parametrize("B,H,S,D,causal,pads,hpads", [
+    (2, 60, 200, 64, True, [0, 0], [0, 0]),
+    (1, 40, 321, 64, False, [4, 12], [1, 0]),
+    (3, 30, 257, 64, True, [0, 32], [3, 1]),
+    (1, 12, 700, 64, True, [12, 4], [0, 3]),
+    (2, 20, 513, 64, False, [0, 0], [0, 2]),
+    (1, 8, 1000, 64, True, [32, 12], [1, 1]),
+    (4, 24, 129, 64, True, [4, 0], [0, 1]),
+])
+def test_w16_backward_many_heads(B, H, S, D, causal, pads, hpads):
+    """S > 128 at D = 64 (attn_bwd_w16: 64 keys per workgroup in 16-key
+    chunks, four workgroups per CU, one dS buffer and two barriers per step)
+    with up to 480 workgroups, ragged S (partial last 16-row chunks and
+    64-key blocks with keys past S), both masks and padded strides on both
+    triples."""
+    _run(700 + B + H + S + D, B, H, S, D, causal, pads, hpads)
+
+
 def _run(seed, B, H, S, D, causal, pads, hpads):
     G.say(f"sweep seed={seed} B={B} H={H} S={S} D={D} causal={causal} pads={pads} hpads={hpads}")
     rng = np.random.default_rng(seed)
