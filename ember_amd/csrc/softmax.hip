@@ -6,9 +6,10 @@
 // and four intermediate tensors.  Here each line along the axis is read once
 // or three times and written once:
 //   m = max over the line (fmaxf: any order gives the same value)
-//   e = expf(x - m),  s = sum of e,  out = e / s
-// with the same fp32 operations per element as the composed path.  Only the
-// order of the sum differs where lines are long: the last axis is reduced
+//   e = expf(x - m),  s = sum of e,  out = e * (1 / s)  (within 2 ulp of e / s)
+// with the composed path's fp32 operations per element, except that the
+// division is a multiply by the line's reciprocal.  The order of the sum also
+// differs where lines are long: the last axis is reduced
 // across a wave or a workgroup in a fixed tree order (deterministic);
 // other axes are summed in index order as sum_axis does.
 //   * last axis, L <= 2048: a wave per row, the row held in registers;
@@ -64,11 +65,13 @@ __global__ __launch_bounds__(256) void softmax_rows_wave(const float *__restrict
         v[j] = e;
         s += e;
     }
-    s = wave_sum(s);
+    // One correctly rounded reciprocal per row and a multiply per element
+    // (within 2 ulp of the quotient) instead of an IEEE division per element.
+    const float inv = 1.0f / wave_sum(s);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = 64 * j + lane;
-        if (c < L) q[c] = v[j] / s;
+        if (c < L) q[c] = v[j] * inv;
     }
 }
 
@@ -118,19 +121,19 @@ __global__ __launch_bounds__(256) void softmax_rows_block(const float *__restric
     } else {
         for (int c = t; c < L; c += 256) s += expf(p[c] - m);
     }
-    s = block_reduce<false>(s, red);
+    const float inv = 1.0f / block_reduce<false>(s, red);
     if (VEC4) {
         for (int c = 4 * t; c < L; c += 1024) {
             const float4 x = *(const float4 *)&p[c];
             float4 y;
-            y.x = expf(x.x - m) / s;
-            y.y = expf(x.y - m) / s;
-            y.z = expf(x.z - m) / s;
-            y.w = expf(x.w - m) / s;
+            y.x = expf(x.x - m) * inv;
+            y.y = expf(x.y - m) * inv;
+            y.z = expf(x.z - m) * inv;
+            y.w = expf(x.w - m) * inv;
             *(float4 *)&q[c] = y;
         }
     } else {
-        for (int c = t; c < L; c += 256) q[c] = expf(p[c] - m) / s;
+        for (int c = t; c < L; c += 256) q[c] = expf(p[c] - m) * inv;
     }
 }
 
@@ -147,9 +150,10 @@ __global__ __launch_bounds__(256) void softmax_lines(const float *__restrict__ a
         for (int r = 1; r < L; ++r) m = fmaxf(m, a[base + (int64_t)r * inner]);
         float s = 0.0f;
         for (int r = 0; r < L; ++r) s += expf(a[base + (int64_t)r * inner] - m);
+        const float inv = 1.0f / s;
         for (int r = 0; r < L; ++r) {
             const int64_t off = base + (int64_t)r * inner;
-            out[off] = expf(a[off] - m) / s;
+            out[off] = expf(a[off] - m) * inv;
         }
     }
 }
