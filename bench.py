@@ -413,8 +413,8 @@ def secondary(L, ev):
     attn("config1_fwd", 1, 4, 256, 64, False, False, 50, kept=True)
     attn("config2_causal_fwd", 8, 16, 2048, 64, True, False, 20, kept=True)
     attn("config5_attention_fwd_bwd", 8, 16, 1024, 64, True, True, 20, det=True)
-    # Config 3's backward once more in deterministic mode (dq partials:
-    # 8 GiB of scratch, released right after).
+    # Config 3's backward once more in deterministic mode (dq added in a
+    # fixed order per tile, a counter per 16 rows).
     attn("config3_deterministic_bwd", 4, 32, 4096, 128, True, True, 5, det=True)
     L.ember_empty_cache()
     for S in (32, 64, 128):  # 2^20 query rows of D=128 per tensor (512 MiB)

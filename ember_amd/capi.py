@@ -85,6 +85,12 @@ def lib() -> C.CDLL:
     L.ember_set_deterministic.restype = None
     L.ember_get_deterministic.argtypes = []
     L.ember_get_deterministic.restype = C.c_int
+    L.ember_deterministic_timeouts.argtypes = []
+    L.ember_deterministic_timeouts.restype = C.c_int
+    L.ember_launch_log_reset.argtypes = []
+    L.ember_launch_log_reset.restype = None
+    L.ember_launch_log.argtypes = []
+    L.ember_launch_log.restype = C.c_char_p
     L.adam_step.restype = C.c_int
     L.adam_step.argtypes = [C.POINTER(_vp)] * 4 + [C.POINTER(_i64), C.c_int] + [C.c_double] * 4 + [_i64]
     L.adamw_step.restype = C.c_int
@@ -98,14 +104,35 @@ def lib() -> C.CDLL:
 def set_deterministic(enabled: bool) -> None:
     """Process-wide switch for bitwise-reproducible results
     (ember_set_deterministic).  Off by default.  With it on, attention_bwd's
-    dq at S > 128 (S > 64 at D = 32) is summed in a fixed key order (a scratch buffer of
-    ceil(S/128)*B*H*S_pad*128 floats and one extra pass) instead of with
-    atomic adds; every other operator is reproducible either way."""
+    dq at S > 128 (S > 64 at D = 32) is added in a fixed key-block order per
+    dQ tile (a counter per 16 rows) instead of in the atomics' arrival
+    order; every other operator is reproducible either way."""
     lib().ember_set_deterministic(1 if enabled else 0)
+
+
+def deterministic_timeouts() -> int:
+    """Deterministic-mode waits for a dQ tile's turn that gave up on the
+    current device (ember_deterministic_timeouts); 0 means every
+    deterministic dQ so far was added in its fixed order.  Synchronises."""
+    n = lib().ember_deterministic_timeouts()
+    if n < 0:
+        check(what="ember_deterministic_timeouts")
+    return n
 
 
 def is_deterministic() -> bool:
     return bool(lib().ember_get_deterministic())
+
+
+def launch_log_reset() -> None:
+    """Clears this thread's log of launched kernels (ember_launch_log_reset)."""
+    lib().ember_launch_log_reset()
+
+
+def launch_log() -> list[str]:
+    """Names of the kernels this thread launched since launch_log_reset()."""
+    text = lib().ember_launch_log().decode()
+    return text.split(",") if text else []
 
 
 def check(status: int | None = None, what: str = "ember_amd") -> None:

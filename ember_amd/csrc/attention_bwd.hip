@@ -18,6 +18,8 @@
 // 2x slower than the VGPR form (and D = 64 causal is 6 % faster in VGPR form).
 #include <mutex>
 
+#include <algorithm>
+
 #include "attention_bwd_kernels.h"
 
 namespace ember {
@@ -662,7 +664,7 @@ int launch_bwd_lds16(const BwdArgs &args, int nbh)
         grid = nbh < ncu ? nbh : ncu;
     }
     hipLaunchKernelGGL((attn_bwd_lds16<D, R, CAUSAL>), dim3((unsigned)grid), dim3(R * 8), 0, 0, args, nbh);
-    return launch_ok("attn_bwd_lds16") ? EMBER_OK : EMBER_ERR_DEVICE;
+    return launch_ok(R == 32 ? "attn_bwd_lds16_r32" : "attn_bwd_lds16_r64") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 template <bool CAUSAL>
@@ -676,51 +678,85 @@ int launch_bwd_short_lds(const BwdArgs &args, int nbh)
 }  // namespace
 }  // namespace ember
 
-// Row statistics of the no-allocation entry point: a fixed device array,
-// one per GPU (each device that loads this library holds its own copy until
-// the process ends).  2^22 floats = 16 MiB, i.e. lse2 and delta for up to
-// 2^21 padded rows (B * H * S_pad).  Host code never uses this name as an
-// address: the device address comes from hipGetSymbolAddress, once per
-// device (noalloc_stats below).
-static __device__ __align__(256) float scratch[size_t(1) << 22];
+// Scratch of the no-allocation entry point: a fixed device array, one per
+// GPU (each device that loads this library holds its own copy until the
+// process ends).  2^22 floats (16 MiB) of row statistics, i.e. lse2 and
+// delta for up to 2^21 padded rows (B * H * S_pad), then 2^17 ints for
+// deterministic mode's tile counters (rows_pad / 16).
+// Host code never uses this name as an address: the device address comes
+// from hipGetSymbolAddress, once per device (noalloc_scratch below).
+constexpr size_t kNoAllocStatsFloats = size_t(1) << 22;
+constexpr size_t kNoAllocOrderInts = size_t(1) << 17;
+static __device__ __align__(256) float scratch[kNoAllocStatsFloats + kNoAllocOrderInts];
+
+// Deterministic mode's count of tile waits that gave up (see
+// attention_bwd_kernels.h), one per GPU, zero when the library loads.
+static __device__ int order_timeouts[1];
 
 namespace ember {
 namespace {
 
-constexpr size_t kNoAllocStatsFloats = size_t(1) << 22;
 constexpr int kNoAllocDevices = 16;
 
-// Where attention_bwd_rows puts the row statistics (2 * rows_pad floats):
-// sets *out and returns EMBER_OK, or returns the status it recorded.
-using StatsSource = int (*)(int64_t rows_pad, float **out);
+// Where attention_bwd_rows puts the row statistics (2 * rows_pad floats)
+// and, when `ordered`, deterministic mode's tile counters (rows_pad / 16
+// ints): sets *stats (and *order) and returns EMBER_OK, or returns the
+// status it recorded.
+using StatsSource = int (*)(int64_t rows_pad, bool ordered, float **stats, int **order);
 
-int library_stats(int64_t rows_pad, float **out)
+int library_stats(int64_t rows_pad, bool ordered, float **stats, int **order)
 {
-    *out = (float *)scratch(kScratchAttnDelta, (size_t)rows_pad * 2 * sizeof(float));
-    return *out ? EMBER_OK : EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
+    *stats = (float *)scratch(kScratchAttnDelta, (size_t)rows_pad * 2 * sizeof(float));
+    if (!*stats) return EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
+    if (ordered) {
+        *order = (int *)scratch(kScratchAttnOrder, (size_t)(rows_pad / 16) * sizeof(int));
+        if (!*order) return EMBER_ERR_OUT_OF_MEMORY;
+    }
+    return EMBER_OK;
 }
 
-std::mutex g_noalloc_mu;
-float *g_noalloc_ptr[kNoAllocDevices];
+// The device address of a __device__ array on the current device, looked up
+// once per device and symbol.
+std::mutex g_symbol_mu;
 
-int noalloc_stats(int64_t rows_pad, float **out)
+template <typename T>
+int symbol_address(T **cache, const void *symbol, const char *what, T **out)
+{
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return EMBER_ERR_DEVICE;
+    if (dev < 0 || dev >= kNoAllocDevices) return record_error(EMBER_ERR_UNSUPPORTED, what);
+    std::lock_guard<std::mutex> lock(g_symbol_mu);
+    T **slot = &cache[dev];
+    if (!*slot) {
+        T *ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress((void **)&ptr, symbol);
+        if (err != hipSuccess || !ptr) return record_error(EMBER_ERR_DEVICE, what, err);
+        *slot = ptr;
+    }
+    *out = *slot;
+    return EMBER_OK;
+}
+
+float *g_noalloc_ptr[kNoAllocDevices];
+int *g_timeouts_ptr[kNoAllocDevices];
+
+int timeouts_ptr(int **out)
+{
+    return symbol_address(g_timeouts_ptr, HIP_SYMBOL(::order_timeouts),
+                          "hipGetSymbolAddress(attention_bwd order_timeouts)", out);
+}
+
+int noalloc_stats(int64_t rows_pad, bool ordered, float **stats, int **order)
 {
     if ((size_t)rows_pad * 2 > kNoAllocStatsFloats)
         return record_error(EMBER_ERR_INVALID_ARGUMENT,
                             "attention_bwd_noalloc: B*H*S_pad (S rounded up to 32) exceeds 2^21 rows");
-    int dev = 0;
-    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return EMBER_ERR_DEVICE;
-    if (dev < 0 || dev >= kNoAllocDevices)
-        return record_error(EMBER_ERR_UNSUPPORTED, "attention_bwd_noalloc: device index");
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    if (!g_noalloc_ptr[dev]) {
-        float *ptr = nullptr;
-        const hipError_t err = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(::scratch));
-        if (err != hipSuccess || !ptr)
-            return record_error(EMBER_ERR_DEVICE, "hipGetSymbolAddress(attention_bwd_noalloc scratch)", err);
-        g_noalloc_ptr[dev] = ptr;
-    }
-    *out = g_noalloc_ptr[dev];
+    float *base = nullptr;
+    const int st = symbol_address(g_noalloc_ptr, HIP_SYMBOL(::scratch),
+                                  "hipGetSymbolAddress(attention_bwd_noalloc scratch)", &base);
+    if (st != EMBER_OK) return st;
+    *stats = base;
+    if (ordered) *order = (int *)(base + kNoAllocStatsFloats);  // rows_pad / 16 <= 2^21 / 16
     return EMBER_OK;
 }
 
@@ -728,7 +764,7 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
                        const float *lse, const float *d_o, float *dq, float *dk, float *dv, int64_t B,
                        int64_t H, int64_t S, int64_t D, float scale, int causal, int64_t in_sb,
                        int64_t in_sh, int64_t in_ss, int64_t out_sb, int64_t out_sh, int64_t out_ss,
-                       StatsSource stats_source, bool noalloc, const char *who)
+                       StatsSource stats_source, const char *who)
 {
     const void *ptrs[] = {q, k, v, o, lse, d_o, dq, dk, dv};
     const int64_t strides[] = {in_sb, in_sh, in_ss, out_sb, out_sh, out_ss};
@@ -759,7 +795,9 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
         sa.dq = dq;
         sa.dk = dk;
         sa.dv = dv;
-        sa.lse2 = sa.delta = sa.dq_part = nullptr;
+        sa.lse2 = sa.delta = nullptr;
+        sa.order = sa.order_timeouts = nullptr;
+        sa.order_group = 1;
         sa.H = (int)H;
         sa.S = (int)S;
         sa.S_pad = sa.nkb = 0;
@@ -792,24 +830,13 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     const int64_t S_pad = (S + kBq - 1) / kBq * kBq;
     const int64_t rows_pad = B * H * S_pad;
     const int64_t nkb = (S + kBk - 1) / kBk;
-    // Deterministic dq: per-key-block partials, summed in a fixed order.
-    float *dq_part = nullptr;
-    if (deterministic()) {
-        if (noalloc)
-            return record_error(EMBER_ERR_UNSUPPORTED,
-                                "attention_bwd_noalloc: deterministic dq at S > 128 (S > 64 at D = 32) "
-                                "needs a scratch buffer (use attention_bwd)");
-        // B*H*S_pad*128*4 < 2^61 (B*H < 2^21, S < 2^30): the product below
-        // cannot wrap once nkb passes this check.
-        if (nkb > INT64_MAX / (B * H * S_pad * kBk * (int64_t)sizeof(float)))
-            return record_error(EMBER_ERR_OUT_OF_MEMORY, "attention_bwd: deterministic dq partials");
-        dq_part = (float *)scratch(kScratchAttnDqPart,
-                                   (size_t)dq_part_floats(nkb, B * H, S_pad) * sizeof(float));
-        if (!dq_part) return EMBER_ERR_OUT_OF_MEMORY;  // scratch() recorded the cause
-    }
+    // Deterministic dq: tile counters (ordered dQ, attention_bwd_kernels.h).
+    const bool ordered = deterministic();
+    int *order = nullptr, *timeouts = nullptr;
     float *stats = nullptr;
-    st = stats_source(rows_pad, &stats);
+    st = stats_source(rows_pad, ordered, &stats, &order);
     if (st != EMBER_OK) return st;
+    if (ordered && (st = timeouts_ptr(&timeouts)) != EMBER_OK) return st;
 
     BwdArgs args;
     args.q = q;
@@ -823,7 +850,24 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
     args.dv = dv;
     args.lse2 = stats;
     args.delta = stats + rows_pad;
-    args.dq_part = dq_part;
+    args.order = order;
+    args.order_timeouts = timeouts;
+    args.order_group = 1;
+    if (ordered && causal) {
+        // Key blocks per group of the dQ order (attention_bwd_kernels.h): as
+        // many as run at once per head, R = slots / heads (B * H rounded up
+        // to the 8 XCDs), while the lower R - 1 key blocks of a group leave
+        // room for its top key block with a sixteenth of the slots spare.
+        // Non-causal walks all start at the first tile, where no key block
+        // is ahead of another: R = 1 (ascending).
+        const int ncu = device_cu_count();
+        const int per_cu = D == 64 ? 4 : D == 32 ? 2 : 1;  // workgroups per CU (LDS, registers)
+        const int64_t slots = (int64_t)ncu * per_cu;
+        const int64_t heads8 = (B * H + 7) / 8 * 8;
+        int64_t R = std::min<int64_t>(nkb, slots / heads8);
+        while (R > 1 && (R - 1) * heads8 + 1 > slots - slots / 16) --R;
+        args.order_group = (int)std::max<int64_t>(1, R);
+    }
     args.H = (int)H;
     args.S = (int)S;
     args.S_pad = (int)S_pad;
@@ -859,17 +903,19 @@ extern "C" int attention_bwd(const float *q, const float *k, const float *v, con
 {
     return ember::attention_bwd_rows(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale, causal, in_sb,
                                      in_sh, in_ss, out_sb, out_sh, out_ss, ember::library_stats,
-                                     false, "attention_bwd");
+                                     "attention_bwd");
 }
 
-// The same computation with the row statistics in the fixed array above:
-// no hipMalloc, hipFree or other allocating call on any path (the first call
-// on a device looks up the array's device address).  Every thread and call
-// on one device shares that device's array; the library enqueues all work on
-// the null stream, so calls run one after another, and launches of this entry
-// point that overlap on one device would race on the array.  Each call writes
-// every statistic it reads (attn_bwd_pre fills all 2 * rows_pad floats,
-// padding rows included) before reading it, so nothing needs clearing.
+// The same computation with the row statistics (and deterministic mode's
+// counters) in the fixed array above: no hipMalloc, hipFree or other
+// allocating call on any path (the first call on a device looks up the
+// array's device address).  Every thread and call on one device shares that
+// device's array; the library enqueues all work on the null stream, so calls
+// run one after another, and launches of this entry point that overlap on one
+// device would race on the array.  Each call writes every statistic and
+// counter it reads (attn_bwd_pre fills all 2 * rows_pad floats, padding rows
+// included, and zeroes the counters) before reading it, so nothing needs
+// clearing.
 extern "C" int attention_bwd_noalloc(const float *q, const float *k, const float *v, const float *o,
                                      const float *lse, const float *d_o, float *dq, float *dk,
                                      float *dv, int64_t B, int64_t H, int64_t S, int64_t D,
@@ -878,5 +924,17 @@ extern "C" int attention_bwd_noalloc(const float *q, const float *k, const float
 {
     return ember::attention_bwd_rows(q, k, v, o, lse, d_o, dq, dk, dv, B, H, S, D, scale, causal, in_sb,
                                      in_sh, in_ss, out_sb, out_sh, out_ss, ember::noalloc_stats,
-                                     true, "attention_bwd_noalloc");
+                                     "attention_bwd_noalloc");
+}
+
+// Deterministic mode's tile waits that gave up on the current device since
+// the library was loaded (attention_bwd_kernels.h); synchronises the device.
+extern "C" int ember_deterministic_timeouts(void)
+{
+    int *ptr = nullptr;
+    if (ember::timeouts_ptr(&ptr) != EMBER_OK) return -1;
+    int v = 0;
+    if (!ember::hip_ok(hipMemcpy(&v, ptr, sizeof(int), hipMemcpyDeviceToHost), "ember_deterministic_timeouts"))
+        return -1;
+    return v;
 }

@@ -24,9 +24,11 @@
 //     dS of all 4 waves goes through LDS so that dQ(32 x D) = dS . K over the
 //     workgroup's 128 keys is one more MFMA product per wave, added to the
 //     global dQ with hardware fp32 atomics (dq must be device memory).
-//     Deterministic mode (ember_set_deterministic) instead stores each
-//     wave's dQ contribution into a partial slab of its own, and a third
-//     launch (attn_bwd_dq_reduce) sums the slabs in ascending key order.
+//     Deterministic mode (ember_set_deterministic) adds the same values with
+//     the same atomics, but in a fixed order: a tile's contributions come in
+//     ascending key-block order, each wave waiting for the tile's counter
+//     to show that the key blocks before its own have added theirs (see
+//     "Ordered dQ" below).
 //     That product is software-pipelined by one block: block j's step runs
 //     the dQ MFMAs of block j-1 in between block j's softmax instructions,
 //     so the matrix core keeps working while the softmax's VALU and
@@ -65,10 +67,14 @@ struct BwdArgs {
     const float *q, *k, *v, *o, *lse, *dout;
     float *dq, *dk, *dv;
     float *lse2, *delta;  // row statistics, (B*H, S_pad) each
-    // Deterministic mode (ember_set_deterministic): dq contributions, one
-    // dense (B*H, S_pad, D) slab per 128 / NSPLIT keys (attn_bwd_dq_reduce
-    // sums them); null otherwise (dq accumulated with atomics).
-    float *dq_part;
+    // Deterministic mode (ember_set_deterministic), null otherwise:
+    // order[bh * (S_pad / 16) + m / 16] counts the contributions added so
+    // far to the dQ rows of head bh from row m (16-row granularity);
+    // attn_bwd_pre zeroes them.  order_timeouts counts waits that gave up (a
+    // device counter that is never reset).
+    int *order;
+    int *order_timeouts;
+    int order_group;  // key blocks per group of the order (see "Ordered dQ")
     int H, S, S_pad, nkb;
     float c;      // scale * log2(e)
     float scale;
@@ -80,11 +86,11 @@ struct BwdArgs {
 int launch_bwd_causal_d128(const BwdArgs &args, int64_t rows_pad, int nblocks);
 
 // attention_bwd_s128.hip: 64 < S <= 128 at D = 64 or 128, one workgroup
-// per head (no row statistics or dq partials: args.lse2, delta, dq_part
+// per head (no row statistics and no atomics: args.lse2, delta, order
 // unused).
 int launch_bwd_s128(const BwdArgs &args, int D, bool causal, int nbh);
-// attention_bwd_w16.hip: D = 64 at S > 128 (attn_bwd_pre, attn_bwd_w16 and,
-// when args.dq_part is set, attn_bwd_dq_reduce).
+// attention_bwd_w16.hip: D = 64 at S > 128 (attn_bwd_pre, then attn_bwd_w16,
+// ordered when args.order is set).
 int launch_bwd_w16(const BwdArgs &args, int64_t rows_pad, bool causal, int nbh);
 
 namespace {
@@ -96,7 +102,8 @@ constexpr int kBk = kBkw * kWaves;  // keys per workgroup
 constexpr int kBq = 32;             // queries per step
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Row statistics and dQ := 0.  D/4 threads per (padded) row.
+// Row statistics and dQ := 0 (and, in deterministic mode, the tile
+// counters := 0).  D/4 threads per (padded) row.
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_pre(BwdArgs a, int64_t rows_pad)
 {
@@ -105,6 +112,7 @@ __global__ __launch_bounds__(256) void attn_bwd_pre(BwdArgs a, int64_t rows_pad)
     const int sub = threadIdx.x % TPR;
     const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
     if (row >= rows_pad) return;  // whole TPR-lane groups retire together
+    if (a.order && sub == 0 && (row & 15) == 0) a.order[row >> 4] = 0;
     const int64_t bh = row / a.S_pad;
     const int m = (int)(row - bh * a.S_pad);
     if (m >= a.S) {
@@ -126,10 +134,85 @@ __global__ __launch_bounds__(256) void attn_bwd_pre(BwdArgs a, int64_t rows_pad)
         a.delta[row] = s;
         a.lse2[row] = a.lse[bh * a.S + m] * kLog2e;
     }
-    if (!a.dq_part) {  // deterministic mode: attn_bwd_dq_reduce writes all of dq
-        const int64_t qoff = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub;
-        *(f32x4 *)(a.dq + qoff) = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int64_t qoff = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub;
+    *(f32x4 *)(a.dq + qoff) = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// ---- Ordered dQ (deterministic mode) ----
+// fp32 addition is not associative, so dQ added with atomics in arrival
+// order differs in its last bits from run to run.  In deterministic mode each
+// dQ tile receives its key blocks' contributions in a fixed order: the wave
+// that adds key block kb's share of a tile first waits until the tile's
+// counter shows that every key block before kb in that order has added
+// its share, then adds its own with the same atomics, waits for their
+// acknowledgement and increments the counter.
+// The order follows the hardware's schedule.  Work items keep the default
+// mode's numbering (key block major, heaviest causal walks first, each
+// head's workgroups on one XCD), and the workgroups of each XCD start in
+// index order.  Key blocks come in groups of R (args.order_group): the
+// groups in ascending order, and within a group descending, because the R
+// key blocks of a group run at the same time and, causally, key block kb + 1
+// starts its walk at the tile key block kb reaches four steps later, so
+// that it is ahead at every tile they share.  A workgroup waits only for
+// lower groups, which started earlier, and for higher key blocks of its own
+// group; the host picks R so that the groups below the top key block of a
+// group fit in the device at once, R <= 1 + (slots - 1) / (B * H) (slots:
+// workgroups resident at once, an eighth kept spare), so the top key blocks,
+// which wait on lower groups only, always start, and no wait can deadlock.
+// The counter is polled a step ahead of its use.  A workgroup first reads
+// the counter of the last tile it adds to: if every key block before it has
+// added its share there, it has added all its tiles (each walks its tiles
+// upward, and a key block that sees one of this workgroup's tiles sees its
+// last one), and the workgroup walks without polls or waits
+// (kDqOrderedFree), only counting its own adds.
+// The adds are released by waiting for their acknowledgement (vmcnt), not by
+// an agent-scope release fence: these atomics are performed where every XCD's
+// atomics on the address meet (adds into one tile from several XCDs are
+// exact), and an acknowledged atomic has been performed there; the fence
+// would add an L2 write-back per wave and step (3.8x the time at B4 H32
+// S4096 D128), and with it and without it dQ came out the same bits in
+// every case measured (causal and not, D = 32, 64, 128).
+// Each wait is still bounded, should those start-order assumptions ever not
+// hold: after ~2 s (s_memrealtime runs at 100 MHz) it gives up, counts
+// itself in order_timeouts, and from then on no wait blocks; the sum stays
+// correct, only its order is lost, which ember_deterministic_timeouts()
+// reports.
+constexpr int kDqAtomic = 0, kDqOrdered = 1, kDqOrderedFree = 2;
+constexpr uint64_t kOrderTimeoutTicks = 200000000ull;
+
+// A tile counter (relaxed, device scope: the load bypasses this XCD's L2,
+// so it sees increments made on other XCDs).
+__device__ __forceinline__ int order_poll(const int *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until *turn >= expect (polled: an earlier read of *turn).
+__device__ __forceinline__ void order_wait(const int *turn, int expect, int polled, int *timeouts)
+{
+    if (__builtin_amdgcn_readfirstlane(polled) < expect) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+            __builtin_amdgcn_s_sleep(2);
+            if (__builtin_amdgcn_readfirstlane(order_poll(turn)) >= expect) break;
+            if (__builtin_amdgcn_readfirstlane(order_poll(timeouts)) != 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kOrderTimeoutTicks) {
+                if ((threadIdx.x & 63) == 0)
+                    __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
     }
+    asm volatile("" ::: "memory");  // the adds that follow stay after the wait
+}
+
+// This wave's adds into the tile have been acknowledged (vmcnt 0: every
+// vector memory operation of the wave has completed); count them.
+__device__ __forceinline__ void order_done(int *turn)
+{
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+    asm volatile("" ::: "memory");
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(turn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D>
@@ -152,12 +235,6 @@ struct BwdLayout {
 
 constexpr int kMaxSlots = 5;  // BwdLayout<128>::SLOTS
 
-// How a workgroup's dQ reaches memory:
-//   kDqAtomic: added into dq with fp32 atomics (dq zeroed by attn_bwd_pre);
-//   kDqPartial: stored into the wave's partial slab (deterministic mode),
-//     summed by attn_bwd_dq_reduce.
-constexpr int kDqAtomic = 0, kDqPartial = 1;
-
 // Buffers for a block's dS: two at D = 64, used by alternate blocks, which
 // saves one barrier per block (bwd_step; +2-3 % at D = 64); one at D = 128
 // (no LDS left) and at D = 32 (two measured -1 to -4 % causal).  The
@@ -170,8 +247,9 @@ constexpr int kDsBufs = D == 64 ? 2 : 1;
 struct BwdBlock {
     const float *qp, *gp;      // q, dO at (b, h)
     const float *l2p, *dlp;    // lse2, delta at (b, h)
-    float *dqp;                // dq at (b, h); deterministic: this wave's dq_part slab at (b, h)
-    int S, nq, n0w, w;
+    float *dqp;                // dq at (b, h)
+    int *turns;                // deterministic mode: tile counters of (b, h)
+    int S, nq, n0w, w, kb;
     int in_ss, out_ss;
     // Per copy slot s (copy t = w + 4s of a tile): this lane's chunk as a
     // byte offset within the block for q and dO (0 for padding or slack:
@@ -264,24 +342,50 @@ __device__ __forceinline__ DqState<D> dq_state(int w)
     return st;
 }
 
-// The finished dQ block (rows m0..m0+31) to memory, by mode (kDqAtomic ...):
-// added into dq, or stored into this wave's partial slab (dense rows of D
-// floats, all 32 rows: the slab has S_pad rows; rows past S hold zeros and
-// are never read).
-template <int D, int DQ>
-__device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, int m0, const f32x16 &qacc)
+// Deterministic mode: the contributions that come before key block kb's at
+// a tile whose last contributing key block is `last` (ordered dQ above):
+// every key block of the lower groups, and those after kb in its own group.
+__device__ __forceinline__ int order_before(int kb, int last, int R)
+{
+    const int g0 = kb - kb % R;
+    return g0 + min(g0 + R - 1, last) - kb;
+}
+
+// How many increments this wave must see on the counter of the tile of rows
+// m0.. before adding: four per key block before kb in the order (one per
+// wave), and, where waves share dQ columns (D < 128), those of the lower
+// waves of its own key block.
+template <int D, bool CAUSAL>
+__device__ __forceinline__ int dq_turn_expect(const BwdArgs &a, const BwdBlock &k, int m0)
+{
+    constexpr int DB = BwdLayout<D>::DB;
+    const int last = CAUSAL ? min(a.nkb - 1, (m0 / kBq) >> 2) : a.nkb - 1;  // key blocks of 128 = 4 tiles
+    return 4 * order_before(k.kb, last, a.order_group) + (k.w / DB) * DB;
+}
+
+// Deterministic mode: whether a wave counts its adds into a tile at once
+// (waves that share dQ columns wait for each other within the step) or
+// after the step's wait for its copies, which then costs no extra wait.
+template <int D>
+constexpr bool kDoneAtOnce = BwdLayout<D>::DB < 4;
+
+// The finished dQ block (rows m0..m0+31) added into dq with atomics;
+// deterministic mode (kDqOrdered) first waits for its turn (polled: an
+// earlier read of the tile counter) and counts its adds (kDoneAtOnce) or
+// leaves that to the caller.
+template <int D, bool CAUSAL, int DQ>
+__device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, int m0, const f32x16 &qacc,
+                                         int polled)
 {
     constexpr int DB = BwdLayout<D>::DB;
     const int lane = threadIdx.x & 63;
     const int h32 = lane >> 5;
     const int l32 = lane & 31;
     const int dblk = k.w % DB;
-    if constexpr (DQ == kDqPartial) {
-        float *pb = k.dqp + (int64_t)m0 * D + 32 * dblk + 4 * h32 * D + l32;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) pb[((i >> 2) * 8 + (i & 3)) * D] = qacc[i] * a.scale;
-        return;
-    }
+    if constexpr (DQ == kDqOrdered)
+        order_wait(k.turns + (m0 >> 4), dq_turn_expect<D, CAUSAL>(a, k, m0), polled, a.order_timeouts);
+    else if constexpr (DQ == kDqOrderedFree)
+        asm volatile("" ::: "memory");
     // Row i of the block: wave-uniform row base + unsigned lane offset.
     float *dqb = k.dqp + (int64_t)m0 * k.in_ss + 32 * dblk;
     const unsigned qoff = (unsigned)(4 * h32 * k.in_ss + l32);
@@ -298,6 +402,7 @@ __device__ __forceinline__ void dq_store(const BwdArgs &a, const BwdBlock &k, in
             if (m0 + acc_row(i, h32) < k.S) unsafeAtomicAdd(rowp + qoff, qacc[i] * a.scale);
         }
     }
+    if constexpr (DQ != kDqAtomic && kDoneAtOnce<D>) order_done(k.turns + (m0 >> 4));
 }
 
 // The dQ product of the previous block (when PREV) fused with this block's
@@ -371,6 +476,9 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
     const float *const ds = dsb + (parity ^ 1) * kDsStride;
     float *const ds_out = dsb + parity * kDsStride;
 
+    // Deterministic mode: the previous block's tile counter, read a step ahead of its use.
+    int polled = 0;
+    if (PREV && DQ == kDqOrdered) polled = order_poll(k.turns + ((m0 - kBq) >> 4));
     if (qb + 1 < k.nq) bwd_fetch<D>(k, m0 + kBq, qn, gn, stn);
 
     // ---- S, dP ----
@@ -417,7 +525,7 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
             pacc[i] = y;
         }
     }
-    if (PREV) dq_store<D, DQ>(a, k, m0 - kBq, qacc);
+    if (PREV) dq_store<D, CAUSAL, DQ>(a, k, m0 - kBq, qacc, polled);
 
     // ---- dV += P^T dO, dK += dS^T Q ----
     {
@@ -445,16 +553,19 @@ __device__ __forceinline__ void bwd_step(const BwdArgs &a, const BwdBlock &k, in
         for (int i = 0; i < 16; ++i) ds_out[sbase + ((i >> 2) * 8 + (i & 3)) * L::SSTR] = pacc[i];
     }
     wait_vmem();  // this wave's copies into (qn, gn, stn) have landed
+    if (PREV && DQ != kDqAtomic && !kDoneAtOnce<D>) order_done(k.turns + ((m0 - kBq) >> 4));
     __syncthreads();
 }
 
 // dQ of the last block (its dS is in LDS after the last step's barrier).
-template <int D, int DQ>
+template <int D, bool CAUSAL, int DQ>
 __device__ __forceinline__ void bwd_last_dq(const BwdArgs &a, const BwdBlock &k, int m0,
                                             const float *__restrict__ ds,
                                             const float *__restrict__ kall)
 {
     typedef BwdLayout<D> L;
+    int polled = 0;
+    if (DQ == kDqOrdered) polled = order_poll(k.turns + (m0 >> 4));
     const DqState<D> dqs = dq_state<D>(k.w);
     f32x16 qacc = zero16();
 #pragma unroll
@@ -463,7 +574,8 @@ __device__ __forceinline__ void bwd_last_dq(const BwdArgs &a, const BwdBlock &k,
 #pragma unroll
         for (int j = 0; j < 4; ++j) qacc = mfma_32x32x2(sf[j], kall[dqs.kbase + (kk + j) * D], qacc);
     }
-    dq_store<D, DQ>(a, k, m0, qacc);
+    dq_store<D, CAUSAL, DQ>(a, k, m0, qacc, polled);
+    if (DQ != kDqAtomic && !kDoneAtOnce<D>) order_done(k.turns + (m0 >> 4));
 }
 
 template <int D, bool CAUSAL, int DQ>
@@ -503,13 +615,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     k.gp = a.dout + out_base;
     k.l2p = a.lse2 + (int64_t)bh * a.S_pad;
     k.dlp = a.delta + (int64_t)bh * a.S_pad;
-    if constexpr (DQ == kDqPartial)
-        k.dqp = a.dq_part + ((int64_t)(kb * L::NSPLIT + w / DB) * BH + bh) * a.S_pad * D;
-    else
-        k.dqp = a.dq + in_base;
+    k.dqp = a.dq + in_base;
+    k.turns = DQ == kDqOrdered ? a.order + (int64_t)bh * (a.S_pad / 16) : nullptr;
     k.S = S;
     k.nq = (S + kBq - 1) / kBq;
     k.w = w;
+    k.kb = kb;
     k.n0w = n0 + kBkw * w;
     k.in_ss = (int)a.in_ss;  // row strides < 2^24, checked on the host
     k.out_ss = (int)a.out_ss;
@@ -570,24 +681,41 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     // Keys past the sequence end: P = 0 whatever the row (see bwd_step).
     // Without a causal mask or such keys no block needs the mask.
     const int tail_bias = k.n0w + l32 >= S ? (1 << 24) : 0;
-    auto walk = [&](auto mask) {
+    auto walk = [&](auto mask, auto mode) {
         constexpr bool M = decltype(mask)::value;
-        bwd_step<D, CAUSAL, false, M, DQ>(a, k, qstart, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1, Kall, kr,
-                                          vr, dvacc, dkacc, tail_bias);
+        constexpr int Q = decltype(mode)::value;
+        bwd_step<D, CAUSAL, false, M, Q>(a, k, qstart, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1, Kall, kr,
+                                         vr, dvacc, dkacc, tail_bias);
         for (int qb = qstart + 1; qb < k.nq; qb += 2) {
-            bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb, Qs1, dOs1, St1, dSs, 1, Qs0, dOs0, St0, Kall, kr,
-                                             vr, dvacc, dkacc, tail_bias);
+            bwd_step<D, CAUSAL, true, M, Q>(a, k, qb, Qs1, dOs1, St1, dSs, 1, Qs0, dOs0, St0, Kall, kr,
+                                            vr, dvacc, dkacc, tail_bias);
             if (qb + 1 < k.nq)
-                bwd_step<D, CAUSAL, true, M, DQ>(a, k, qb + 1, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1,
-                                                 Kall, kr, vr, dvacc, dkacc, tail_bias);
+                bwd_step<D, CAUSAL, true, M, Q>(a, k, qb + 1, Qs0, dOs0, St0, dSs, 0, Qs1, dOs1, St1,
+                                                Kall, kr, vr, dvacc, dkacc, tail_bias);
         }
     };
-    if (CAUSAL || k.key_tail)
-        walk(std::true_type{});
-    else
-        walk(std::false_type{});
-    bwd_last_dq<D, DQ>(a, k, (k.nq - 1) * kBq,
-                        dSs + ((k.nq - 1 - qstart) & 1) * (kDsBufs<D> - 1) * kBq * L::SSTR, Kall);
+    const float *const ds_last = dSs + ((k.nq - 1 - qstart) & 1) * (kDsBufs<D> - 1) * kBq * L::SSTR;
+    auto walk_all = [&](auto mode) {
+        if (CAUSAL || k.key_tail)
+            walk(std::true_type{}, mode);
+        else
+            walk(std::false_type{}, mode);
+        bwd_last_dq<D, CAUSAL, decltype(mode)::value>(a, k, (k.nq - 1) * kBq, ds_last, Kall);
+    };
+    if constexpr (DQ == kDqAtomic) {
+        walk_all(std::integral_constant<int, kDqAtomic>{});
+    } else {
+        // Deterministic mode: whether the key blocks before this one have
+        // added their share of its last tile, and so of all its tiles
+        // (ordered dQ above); waves that share dQ columns (D < 128) always
+        // wait for each other.
+        const int m_last = (k.nq - 1) * kBq;
+        const int seen = order_poll(k.turns + (m_last >> 4));
+        if (!kDoneAtOnce<D> && __builtin_amdgcn_readfirstlane(seen) >= dq_turn_expect<D, CAUSAL>(a, k, m_last))
+            walk_all(std::integral_constant<int, kDqOrderedFree>{});
+        else
+            walk_all(std::integral_constant<int, kDqOrdered>{});
+    }
 
     // dK (scaled) and dV rows of this wave's keys: register i -> key
     // n0w + acc_row(i, h32), lane -> d = DB*l32 + db.
@@ -613,51 +741,9 @@ __global__ __launch_bounds__(kThreads, 1) void attn_bwd_kernel(BwdArgs a)
     }
 }
 
-// Deterministic mode's second pass: dq[b, h, m, :] = the sum of the partial
-// slabs in ascending key order (slab j holds keys KPS * j .. KPS * j + KPS - 1,
-// KPS = 128/NSPLIT; causal: only the slabs that start at or before row m,
-// every one of which the main kernel wrote for that row; non-causal: the
-// slabs that start inside the sequence), one thread per 4 floats.  The order
-// is fixed, so dq is bitwise reproducible.
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dq_reduce(BwdArgs a, int BH)
-{
-    constexpr int TPR = D / 4;
-    constexpr int KPS = kBk / BwdLayout<D>::NSPLIT;  // keys per slab
-    const int64_t slab = (int64_t)BH * a.S_pad * D;  // floats per slab
-    const int64_t n = (int64_t)BH * a.S * TPR;
-    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < n;
-         idx += (int64_t)gridDim.x * 256) {
-        const int sub = (int)(idx % TPR);
-        const int64_t row = idx / TPR;
-        const int bh = (int)(row / a.S);
-        const int m = (int)(row - (int64_t)bh * a.S);
-        const int nslab = CAUSAL ? m / KPS + 1 : (a.S + KPS - 1) / KPS;
-        const float *p = a.dq_part + ((int64_t)bh * a.S_pad + m) * D + 4 * sub;
-        f32x4 acc = *(const f32x4 *)p;
-        for (int j = 1; j < nslab; ++j) {
-            const f32x4 x = *(const f32x4 *)(p + j * slab);
-            acc[0] += x[0];
-            acc[1] += x[1];
-            acc[2] += x[2];
-            acc[3] += x[3];
-        }
-        const int b = bh / a.H;
-        const int hh = bh - b * a.H;
-        *(f32x4 *)(a.dq + (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh + (int64_t)m * a.in_ss + 4 * sub) = acc;
-    }
-}
-
-// Floats of the deterministic mode's dq partials: one (B*H, S_pad, D) slab
-// per 128 / NSPLIT keys, i.e. nkb * B*H * S_pad * 128 for every D.
-inline int64_t dq_part_floats(int64_t nkb, int64_t BH, int64_t S_pad)
-{
-    return nkb * BH * S_pad * (int64_t)kBk;
-}
-
-// Launches the backward for args: attn_bwd_pre and the workgroup kernel,
-// whose dQ is atomic or (args.dq_part set) partial, then
-// attn_bwd_dq_reduce.
+// Launches the backward for args: attn_bwd_pre, then the workgroup kernel,
+// whose dQ is added with atomics in arrival order or (args.order set) in
+// key-block order.
 template <int D, bool CAUSAL>
 int launch_bwd(const BwdArgs &args, int64_t rows_pad, int nblocks)
 {
@@ -665,19 +751,13 @@ int launch_bwd(const BwdArgs &args, int64_t rows_pad, int nblocks)
     const int pre_blocks = (int)((rows_pad + RPB - 1) / RPB);
     hipLaunchKernelGGL((attn_bwd_pre<D>), dim3(pre_blocks), dim3(256), 0, 0, args, rows_pad);
     if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
-    if (!args.dq_part) {
+    if (!args.order) {
         hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL, kDqAtomic>), dim3(nblocks), dim3(kThreads), 0, 0,
                            args);
         return launch_ok("attn_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
-    hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL, kDqPartial>), dim3(nblocks), dim3(kThreads), 0, 0, args);
-    if (!launch_ok("attn_bwd_kernel")) return EMBER_ERR_DEVICE;
-    const int BH = nblocks / args.nkb;
-    const int64_t n = (int64_t)BH * args.S * (D / 4);
-    const int64_t want = (n + 255) / 256;
-    const int grid = (int)(want < 16384 ? want : 16384);
-    hipLaunchKernelGGL((attn_bwd_dq_reduce<D, CAUSAL>), dim3(grid), dim3(256), 0, 0, args, BH);
-    return launch_ok("attn_bwd_dq_reduce") ? EMBER_OK : EMBER_ERR_DEVICE;
+    hipLaunchKernelGGL((attn_bwd_kernel<D, CAUSAL, kDqOrdered>), dim3(nblocks), dim3(kThreads), 0, 0, args);
+    return launch_ok("attn_bwd_kernel") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 }  // namespace

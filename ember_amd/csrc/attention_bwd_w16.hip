@@ -31,10 +31,10 @@
 //     LDS; dV += P^T dO, dK += dS^T Q with the P / dS accumulators as the A
 //     operands;
 //   barrier.
-// dQ goes out with atomics, or (deterministic mode) into slab kb of the
-// partials, which attn_bwd_dq_reduce sums in key order: the workgroup's 64
-// keys are exactly the 64 keys of that slab at D = 64, and it writes the slab
-// for every row at or after its first key (causal) or every row.
+// dQ goes out with atomics; in deterministic mode with the same atomics in a
+// fixed key-block order per 16-row chunk (ordered dQ,
+// attention_bwd_kernels.h): the chunk's counter is polled a step before the
+// adds, which wait for it to show the key blocks before this one.
 #include "attention_bwd_kernels.h"
 
 namespace ember {
@@ -225,31 +225,31 @@ __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
             }
         }
     };
-    // dQ of chunk qc to memory (register r of block q: row 16 qc + 4g + r,
-    // column 16 (QB w + q) + n): added into dq, or stored into slab kb.
-    auto store_dq = [&](int qc, const f32x4 (&acc)[QB]) {
-        float *__restrict__ dqb;
-        int64_t rs;
-        if constexpr (DQ == kDqPartial) {
-            static_assert(D == 64, "slab kb holds this workgroup's keys only at D = 64");
-            dqb = a.dq_part + ((int64_t)kb * BH + bh) * a.S_pad * D + 16 * QB * w + n;
-            rs = D;
-        } else {
-            dqb = a.dq + in_base + 16 * QB * w + n;
-            rs = in_ss;
-        }
+    // dQ of chunk qc added into dq (register r of block q: row 16 qc + 4g + r,
+    // column 16 (QB w + q) + n).  Deterministic mode (kDqOrdered): first wait
+    // until the chunk's counter (polled: an earlier read) shows the four
+    // waves of every key block before kb in the order; the caller counts the
+    // adds.
+    int *const turns = DQ == kDqOrdered ? a.order + (int64_t)bh * (a.S_pad / 16) : nullptr;
+    // Increments chunk qc's counter must show before this wave adds (ordered
+    // dQ, attention_bwd_kernels.h): four per key block before kb.
+    auto expect = [&](int qc) {
+        const int last = CAUSAL ? min(nkb - 1, qc >> 2) : nkb - 1;  // key blocks of 64 = 4 chunks
+        return 4 * order_before(kb, last, a.order_group);
+    };
+    auto store_dq = [&](auto mode, int qc, const f32x4 (&acc)[QB], int polled) {
+        constexpr int Q = decltype(mode)::value;
+        if constexpr (Q == kDqOrdered)
+            order_wait(turns + qc, expect(qc), polled, a.order_timeouts);
+        else if constexpr (Q == kDqOrderedFree)
+            asm volatile("" ::: "memory");
+        float *__restrict__ dqb = a.dq + in_base + 16 * QB * w + n;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = 16 * qc + 4 * g + r;
             if (row < S) {
 #pragma unroll
-                for (int q = 0; q < QB; ++q) {
-                    const float x = acc[q][r] * a.scale;
-                    if constexpr (DQ == kDqPartial)
-                        dqb[row * rs + 16 * q] = x;
-                    else
-                        unsafeAtomicAdd(dqb + row * rs + 16 * q, x);
-                }
+                for (int q = 0; q < QB; ++q) unsafeAtomicAdd(dqb + row * in_ss + 16 * q, acc[q][r] * a.scale);
             }
         }
     };
@@ -261,24 +261,50 @@ __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
     wait_vmem();
     __syncthreads();
 
-    f32x4 qa[QB];  // dQ of chunk qc - 1, added in step qc + 1
+    // The walk over query chunks; mode: kDqAtomic, or in deterministic mode
+    // kDqOrdered (poll and wait) or kDqOrderedFree (every key block before
+    // kb has added all its chunks: no polls or waits).
+    auto walk = [&](auto mode) {
+        constexpr int Q = decltype(mode)::value;
+        constexpr bool POLL = Q == kDqOrdered, COUNT = Q != kDqAtomic;
+        f32x4 qa[QB];  // dQ of chunk qc - 1, added in step qc + 1
 #pragma unroll
-    for (int q = 0; q < QB; ++q) qa[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int qc = qstart; qc < nch; ++qc) {
-        const int st = (qc - qstart) & 1;
-        if (qc >= qstart + 2) store_dq(qc - 2, qa);
-        if (qc + 1 < nch) fetch(qc + 1, sets + (st ^ 1) * L::SET);
-        if (qc >= qstart + 1) dq_product(qc - 1, dsb, qa);
-        __syncthreads();  // every wave has read dS of chunk qc - 1
-        if (kvalid && (!CAUSAL || kc <= qc)) products(qc, sets + st * L::SET, dsb);
-        wait_vmem();      // this wave's copies of chunk qc + 1 have landed
-        __syncthreads();  // dS of chunk qc and all of chunk qc + 1 in LDS
-    }
-    if (nch - qstart >= 2) store_dq(nch - 2, qa);
-    {
-        f32x4 ql[QB];
-        dq_product(nch - 1, dsb, ql);
-        store_dq(nch - 1, ql);
+        for (int q = 0; q < QB; ++q) qa[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        int polled = 0;  // kDqOrdered: the counter of the chunk added next
+        if (POLL) polled = order_poll(turns + qstart);
+        for (int qc = qstart; qc < nch; ++qc) {
+            const int st = (qc - qstart) & 1;
+            if (qc >= qstart + 2) store_dq(mode, qc - 2, qa, polled);
+            if (POLL && qc >= qstart + 1) polled = order_poll(turns + qc - 1);
+            if (qc + 1 < nch) fetch(qc + 1, sets + (st ^ 1) * L::SET);
+            if (qc >= qstart + 1) dq_product(qc - 1, dsb, qa);
+            __syncthreads();  // every wave has read dS of chunk qc - 1
+            if (kvalid && (!CAUSAL || kc <= qc)) products(qc, sets + st * L::SET, dsb);
+            wait_vmem();      // this wave's copies of chunk qc + 1 have landed
+            if (COUNT && qc >= qstart + 2) order_done(turns + qc - 2);
+            __syncthreads();  // dS of chunk qc and all of chunk qc + 1 in LDS
+        }
+        if (nch - qstart >= 2) {
+            store_dq(mode, nch - 2, qa, polled);
+            if (COUNT) order_done(turns + nch - 2);
+        }
+        {
+            f32x4 ql[QB];
+            if (POLL) polled = order_poll(turns + nch - 1);
+            dq_product(nch - 1, dsb, ql);
+            store_dq(mode, nch - 1, ql, polled);
+            if (COUNT) order_done(turns + nch - 1);
+        }
+    };
+    if constexpr (DQ == kDqAtomic) {
+        walk(std::integral_constant<int, kDqAtomic>{});
+    } else {
+        // Whether the key blocks before this one have added their share of
+        // its last chunk, and so of all its chunks (each walks upward).
+        if (__builtin_amdgcn_readfirstlane(order_poll(turns + nch - 1)) >= expect(nch - 1))
+            walk(std::integral_constant<int, kDqOrderedFree>{});
+        else
+            walk(std::integral_constant<int, kDqOrdered>{});
     }
 
     // dK (scaled) and dV of this wave's keys: register r of block 4h + j
@@ -314,17 +340,11 @@ int launch_w16(const BwdArgs &args, int64_t rows_pad, int nbh)
     if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
     const int nkb = (args.S + W16Shape<D>::KB - 1) / W16Shape<D>::KB;
     const dim3 grid((unsigned)(nkb * nbh));
-    if (!args.dq_part) {
+    if (!args.order)
         hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqAtomic>), grid, dim3(256), 0, 0, args, nkb);
-        return launch_ok("attn_bwd_w16") ? EMBER_OK : EMBER_ERR_DEVICE;
-    }
-    hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqPartial>), grid, dim3(256), 0, 0, args, nkb);
-    if (!launch_ok("attn_bwd_w16")) return EMBER_ERR_DEVICE;
-    const int64_t n = (int64_t)nbh * args.S * (D / 4);
-    const int64_t want = (n + 255) / 256;
-    hipLaunchKernelGGL((attn_bwd_dq_reduce<D, CAUSAL>), dim3((unsigned)(want < 16384 ? want : 16384)), dim3(256), 0, 0,
-                       args, nbh);
-    return launch_ok("attn_bwd_dq_reduce") ? EMBER_OK : EMBER_ERR_DEVICE;
+    else
+        hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqOrdered>), grid, dim3(256), 0, 0, args, nkb);
+    return launch_ok("attn_bwd_w16") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 }  // namespace

@@ -939,7 +939,7 @@ int launch_fwd(FwdArgs args, int64_t nbh)
             const int64_t items = (int64_t)(args.nqb + 1) / 2 * nbh;
             hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, true>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
                                dim3(kThreads), 0, 0, args);
-            return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
+            return launch_ok("attn_fwd_wave_pair") ? EMBER_OK : EMBER_ERR_DEVICE;
         }
     }
     if (args.S > 64) {
@@ -965,13 +965,14 @@ int launch_fwd(FwdArgs args, int64_t nbh)
     }
     if constexpr (D < 128) {
         args.nqb = 1;
-        if (args.S <= 32)
+        if (args.S <= 32) {
             hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 4, 32>), dim3((unsigned)((nbh + 3) / 4)),
                                dim3(kThreads), 0, 0, args);
-        else
-            hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 2, 64>), dim3((unsigned)((nbh + 1) / 2)),
-                               dim3(kThreads), 0, 0, args);
-        return launch_ok("attn_fwd_packed") ? EMBER_OK : EMBER_ERR_DEVICE;
+            return launch_ok("attn_fwd_packed_hp4") ? EMBER_OK : EMBER_ERR_DEVICE;
+        }
+        hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 2, 64>), dim3((unsigned)((nbh + 1) / 2)),
+                           dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_packed_hp2") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
     return EMBER_OK;  // not reached: D = 128 always takes the wave kernel above
 }
@@ -986,7 +987,9 @@ int check_attention_args(const void *const *ptrs, int nptrs, int64_t B, int64_t 
     if (B < 0 || H < 0 || S < 0 || D <= 0 || !(scale >= 0.0f) || isinf(scale))
         return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     if (D != 32 && D != 64 && D != 128) return record_error(EMBER_ERR_UNSUPPORTED, who);
-    if (S > (int64_t)INT32_MAX / 2 || B * H > (int64_t)INT32_MAX / 1024)
+    // Each factor is bounded before any product is formed (B, H < 2^31 keep
+    // B * H below 2^62).
+    if (B > INT32_MAX || H > INT32_MAX || S > (int64_t)INT32_MAX / 2 || B * H > (int64_t)INT32_MAX / 1024)
         return record_error(EMBER_ERR_INVALID_ARGUMENT, who);
     // At most 2^33 elements (32 GiB) per tensor: the backward's nine tensors
     // then fill an MI355X's 288 GB, and every launch's grid stays below 2^32

@@ -32,7 +32,7 @@ enum ScratchSlot {
     kScratchLayerNorm = 2,
     kScratchColSum = 3,
     kScratchGemmSplit = 4,
-    kScratchAttnDqPart = 5,
+    kScratchAttnOrder = 5,
     kScratchSlots = 6
 };
 

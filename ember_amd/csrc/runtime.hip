@@ -23,6 +23,7 @@
 // hipMalloc / hipFree per call, the reference's behaviour).
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <atomic>
 #include <map>
@@ -54,8 +55,34 @@ bool hip_ok(hipError_t err, const char *what)
     return false;
 }
 
+// Names of the kernels this thread launched since the last
+// ember_launch_log_reset, comma-separated; a name that does not fit is
+// dropped and the log ends in "...".
+namespace {
+constexpr int kLaunchLogBytes = 1024;
+thread_local char t_launch_log[kLaunchLogBytes];
+thread_local int t_launch_log_len = 0;
+thread_local bool t_launch_log_full = false;
+
+void log_launch(const char *kernel)
+{
+    if (t_launch_log_full) return;
+    const size_t n = strlen(kernel);
+    const int sep = t_launch_log_len ? 1 : 0;
+    if (t_launch_log_len + sep + (int)n + 4 >= kLaunchLogBytes) {
+        memcpy(t_launch_log + t_launch_log_len, "...", 4);
+        t_launch_log_full = true;
+        return;
+    }
+    if (sep) t_launch_log[t_launch_log_len++] = ',';
+    memcpy(t_launch_log + t_launch_log_len, kernel, n + 1);
+    t_launch_log_len += (int)n;
+}
+}  // namespace
+
 bool launch_ok(const char *kernel)
 {
+    log_launch(kernel);
     return hip_ok(hipGetLastError(), kernel);
 }
 
@@ -302,6 +329,18 @@ void ember_empty_cache(void)
         ember::release_cached(dev);
     }
     ember::release_scratch(dev);
+}
+
+void ember_launch_log_reset(void)
+{
+    ember::t_launch_log_len = 0;
+    ember::t_launch_log_full = false;
+    ember::t_launch_log[0] = '\0';
+}
+
+const char *ember_launch_log(void)
+{
+    return ember::t_launch_log;
 }
 
 void ember_set_deterministic(int enabled)

@@ -150,10 +150,11 @@ __global__ __launch_bounds__(256) void softmax_lines(const float *__restrict__ a
         for (int r = 1; r < L; ++r) m = fmaxf(m, a[base + (int64_t)r * inner]);
         float s = 0.0f;
         for (int r = 0; r < L; ++r) s += expf(a[base + (int64_t)r * inner] - m);
-        const float inv = 1.0f / s;
+        // An IEEE division per element, as Ember's composition (a strided
+        // line is latency-bound, so the reciprocal would save nothing here).
         for (int r = 0; r < L; ++r) {
             const int64_t off = base + (int64_t)r * inner;
-            out[off] = expf(a[off] - m) * inv;
+            out[off] = expf(a[off] - m) / s;
         }
     }
 }

@@ -75,12 +75,31 @@ void ember_memory_stats(size_t *in_use, size_t *cached, size_t *peak);
 /* Bitwise-reproducible results (no reference counterpart: the reference
  * has no operator whose result depends on timing).  Off by default.  The
  * only such operator here is attention_bwd's dq at S > 128 (S > 64 at
- * D = 32); with the switch on it is formed in a fixed order instead, at the cost of a
- * scratch buffer and one extra pass.  Every other operator of this library
+ * D = 32); with the switch on its atomic adds are made in a fixed order
+ * instead (per-tile counters; see attention_bwd).  Every other operator of this library
  * is reproducible either way.  The switch is process-wide; set it between
  * calls, not while another thread is inside the library. */
 void ember_set_deterministic(int enabled);
 int ember_get_deterministic(void);
+/* Deterministic mode's waits for a dq tile's turn that gave up, on the
+ * current device since the library was loaded (0 on success; -1 and a
+ * recorded error if the device cannot be read).  A wait gives up only after
+ * about 2 s; the sum is then still complete, but its order is the arrival
+ * order, so 0 means every deterministic dq was added in its fixed order.
+ * Synchronises the device.  No reference counterpart. */
+int ember_deterministic_timeouts(void);
+
+/* Launch log, for tests and profiling scripts that must know which kernel
+ * a call ran (the attention entry points pick one of several kernels by
+ * sequence length, head dimension and launch size).  No reference
+ * counterpart.  ember_launch_log returns the names of the kernels the
+ * calling thread has launched through this library since its last
+ * ember_launch_log_reset, comma-separated in launch order (at most about
+ * 1 KiB; a log that would grow past that ends in "...").  The string
+ * belongs to the library and stays valid until the thread's next library
+ * call. */
+void ember_launch_log_reset(void);
+const char *ember_launch_log(void);
 
 /* ---- random tensors: replaces src/random/distributions.h:8-9 ----
  * (distributions_gpu.cu:11-32; called by src/random/random_api.c:70,88.)
@@ -171,17 +190,17 @@ int attention_fwd(const float *q, const float *k, const float *v, float *o, floa
  * cached between calls.
  * Determinism: dk and dv are bitwise reproducible.  For S > 128 (S > 64 at
  * D = 32), dq is accumulated in HBM with fp32 atomic adds from every key
- * block (128 keys) that sees a query row, so its last bits vary from run to
- * run (each run within the stated tolerance).  At S <= 64, and at S <= 128
- * with D = 64 or 128 (one workgroup per head, which forms each element of
- * dq whole), dq is stored once and reproducible too.  Because of the atomics dq must be
- * device memory (not host or managed memory), and dq must not overlap q, k,
- * v, o, lse, d_o, dk or dv.
- * With ember_set_deterministic(1), the atomic cases instead store each key
- * block's dq contribution in a scratch buffer of nkb*B*H*S_pad*128 floats
- * (nkb = S/128 rounded up; 8 GiB at B4 H32 S4096 D128) and sum them per row
- * in ascending key-block order in a second kernel: dq is then bitwise
- * reproducible, and dk, dv are the same bits as without the switch. */
+ * block (128 keys; 64 at D = 64) that sees a query row, so its last bits
+ * vary from run to run (each run within the stated tolerance).  At S <= 64,
+ * and at S <= 128 with D = 64 or 128 (one workgroup per head, which forms
+ * each element of dq whole), dq is stored once and reproducible too.
+ * Because of the atomics dq must be device memory (not host or managed
+ * memory), and dq must not overlap q, k, v, o, lse, d_o, dk or dv.
+ * With ember_set_deterministic(1), the atomic cases add each dq tile's
+ * key-block contributions in a fixed order (highest key block first), each
+ * key block waiting on a per-tile counter for its turn: dq is then bitwise
+ * reproducible, and dk, dv are the same bits as without the switch.  Extra
+ * scratch: B*H*S_pad/16 ints. */
 int attention_bwd(const float *q, const float *k, const float *v, const float *o,
                   const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                   int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,
@@ -190,23 +209,21 @@ int attention_bwd(const float *q, const float *k, const float *v, const float *o
 
 /* attention_bwd without any device allocation.  No counterpart in the
  * reference.  It is for callers that cannot allocate device memory during the
- * call: code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc.  Same arguments, kernels, results and errors as
- * attention_bwd, except where the row statistics live: a fixed 16 MiB device
- * array inside the library, one per GPU, held until the process ends, instead
- * of library-allocated scratch.  Limit: B*H*S_pad <= 2^21 rows (S_pad = S
+ * call: tight serving loops and harnesses that forbid hipMalloc.  Same
+ * arguments, kernels, results and errors as attention_bwd, also in
+ * deterministic mode, except where the row statistics and deterministic
+ * mode's tile counters live: a fixed device array of 16.5 MiB inside the
+ * library, one per GPU, held until the process ends, instead of
+ * library-allocated scratch.  Limit: B*H*S_pad <= 2^21 rows (S_pad = S
  * rounded up to 32); a larger call returns EMBER_ERR_INVALID_ARGUMENT and
  * launches nothing (S <= 64, and S <= 128 at D = 64 or 128, need no
- * statistics and so no array space).
- * Every call on one GPU shares that GPU's array.  Calls
- * are ordered because all library work runs on the null stream; launches of
- * this entry point that overlap on one GPU (for example replayed on several
- * streams at once) race on the array.  Each call writes every statistic it
- * reads before reading it, so nothing carries over between calls.
- * With ember_set_deterministic(1), where attention_bwd would use the dq
- * partials (S > 128, or S > 64 at D = 32) it returns
- * EMBER_ERR_UNSUPPORTED and launches nothing: they need a buffer of the
- * problem's size. */
+ * statistics and so no array space).  Like every entry point here it
+ * enqueues on the null stream, which cannot be captured into a HIP graph.
+ * Every call on one GPU shares that GPU's array.  Calls are ordered because
+ * all library work runs on the null stream; launches of this entry point
+ * that overlap on one GPU would race on the array.  Each call writes every
+ * statistic and counter it reads before reading it, so nothing carries over
+ * between calls. */
 int attention_bwd_noalloc(const float *q, const float *k, const float *v, const float *o,
                           const float *lse, const float *d_o, float *dq, float *dk, float *dv,
                           int64_t B, int64_t H, int64_t S, int64_t D, float scale, int causal,

@@ -47,7 +47,9 @@ def download_padded(dev, strides, shape):
     return np.array(view), buf
 
 
-def attention_fwd(q, k, v, causal, scale=None):
+def attention_fwd(q, k, v, causal, scale=None, log=None):
+    """O, LSE of the HIP forward.  If `log` is a list, the names of the
+    kernels the call launched are appended to it."""
     B, H, S, D = q.shape
     scale = scale_for(D) if scale is None else scale
     say(f"attention_fwd B={B} H={H} S={S} D={D} causal={causal}")
@@ -55,21 +57,29 @@ def attention_fwd(q, k, v, causal, scale=None):
     o = DeviceArray((B, H, S, D))
     lse = DeviceArray((B, H, S))
     st = capi.contiguous_strides(B, H, S, D)
+    capi.launch_log_reset()
     rc = capi.lib().attention_fwd(dq.ptr, dk.ptr, dv.ptr, o.ptr, lse.ptr, B, H, S, D, scale,
                                   int(causal), *st, *st)
+    if log is not None:
+        log.extend(capi.launch_log())
     capi.check(rc, "attention_fwd")
     return o.numpy(), lse.numpy()
 
 
-def attention_bwd(q, k, v, o, lse, d_o, causal, scale=None):
+def attention_bwd(q, k, v, o, lse, d_o, causal, scale=None, log=None):
+    """dQ, dK, dV of the HIP backward.  If `log` is a list, the names of the
+    kernels the call launched are appended to it."""
     B, H, S, D = q.shape
     scale = scale_for(D) if scale is None else scale
     say(f"attention_bwd B={B} H={H} S={S} D={D} causal={causal}")
     ins = [DeviceArray.from_numpy(x) for x in (q, k, v, o, lse, d_o)]
     outs = [DeviceArray((B, H, S, D)) for _ in range(3)]
     st = capi.contiguous_strides(B, H, S, D)
+    capi.launch_log_reset()
     rc = capi.lib().attention_bwd(*(x.ptr for x in ins), *(x.ptr for x in outs), B, H, S, D,
                                   scale, int(causal), *st, *st)
+    if log is not None:
+        log.extend(capi.launch_log())
     capi.check(rc, "attention_bwd")
     return tuple(x.numpy() for x in outs)
 

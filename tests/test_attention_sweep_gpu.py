@@ -117,12 +117,19 @@ def test_short_backward_walks_many_heads(B, H, S, D, causal, pads, hpads):
     (1, 513, 80, 64, True, [32, 12], [0, 1]),
     (3, 97, 65, 64, False, [0, 4], [3, 3]),
     (2, 128, 100, 64, True, [12, 12], [1, 1]),
+    (2, 200, 72, 128, True, [0, 4], [1, 0]),
+    (3, 120, 100, 128, False, [12, 0], [0, 3]),
+    (1, 517, 80, 128, True, [4, 4], [2, 1]),
 ])
 def test_s128_backward_many_heads(B, H, S, D, causal, pads, hpads):
     """64 < S <= 128 at D = 64 and 128 (attn_bwd_s128: 16-key chunks dealt
     out over the waves, the row statistics formed in the kernel, dQ stored
     directly) with 256 to 600 heads, ragged S (one to eight 16-row chunks,
-    partial last chunks) and padded strides on both triples."""
+    partial last chunks) and padded strides on both triples.  At D = 128 one
+    workgroup per CU walks the heads; with more heads than CUs and an odd
+    chunk count (S = 72, 80, 100: 5 or 7 chunks) a workgroup starts its
+    second head on the other LDS set and dS half, with the previous head's
+    dQ, dK and dV stores still deferred."""
     _run(500 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 

@@ -77,14 +77,18 @@ def test_attention_rejects_bad_layouts():
     # More than 2^33 elements per tensor (B*H*S*D = 2^34): rejected before any
     # device work, so that no launch's grid can pass 2^32 work-items.
     assert _fwd_call(B=1, H=1 << 10, S=1 << 17, D=128) == 1
+    # Factors whose product would overflow int64 are rejected one by one.
+    assert _fwd_call(B=1 << 40, H=1 << 40) == 1
+    assert _fwd_call(B=1 << 62, H=4) == 1
+    assert _fwd_call(B=3, H=(1 << 62) + 1) == 1
     L.ember_get_last_error()
     assert _fwd_call(S=0) == 0                         # empty: nothing to do
 
 
-def test_deterministic_switch_and_noalloc_refusal():
+def test_deterministic_switch_and_noalloc_limit():
     """ember_set_deterministic is host state (no device call); with it on,
-    attention_bwd_noalloc refuses S > 128 (its dq partials would need a
-    buffer) before any device work, and still accepts the empty problem."""
+    attention_bwd_noalloc still checks its row limit (B*H*S_pad <= 2^21)
+    before any device work, and still accepts the empty problem."""
     L = capi.lib()
     assert capi.is_deterministic() is False
     p = C.c_void_p(16)
@@ -92,8 +96,9 @@ def test_deterministic_switch_and_noalloc_refusal():
     try:
         capi.set_deterministic(True)
         assert L.ember_get_deterministic() == 1
-        assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 200, 64, 0.125, 1, *st, *st) == 2
-        assert L.ember_get_last_error() == 2
+        # 2^15 heads of S = 200 (S_pad 224): 7.3 M rows > 2^21.
+        assert L.attention_bwd_noalloc(*[p] * 9, 1, 1 << 15, 200, 64, 0.125, 1, *st, *st) == 1
+        assert L.ember_get_last_error() == 1
         assert L.attention_bwd_noalloc(*[p] * 9, 1, 1, 0, 64, 0.125, 1, *st, *st) == 0
     finally:
         capi.set_deterministic(False)
@@ -147,3 +152,28 @@ def test_reference_bindings_link_against_the_library():
         dyn = subprocess.run(["readelf", "-d", os.path.join(link, mod)], check=True, capture_output=True,
                              text=True).stdout
         assert "[libember_amd.so]" in dyn, mod
+
+
+def test_mask_tests_reach_every_attention_kernel():
+    """tests/test_mask_bitwise_gpu.py names a launch shape for every attention
+    kernel the sources launch (the names passed to launch_ok, which the
+    launch log records), so a kernel added later without a bitwise mask
+    check fails here."""
+    import test_mask_bitwise_gpu as M
+
+    names = set()
+    csrc = os.path.join(ROOT, "ember_amd", "csrc")
+    for f in os.listdir(csrc):
+        if f.startswith("attention"):
+            with open(os.path.join(csrc, f)) as fh:
+                for line in fh:
+                    if "launch_ok(" in line:
+                        names.update(re.findall(r'"(attn_\w+)"', line))
+    helpers = {"attn_bwd_pre", "attn_bwd_dq_reduce"}   # row statistics and the slab sum: no mask
+    assert names - helpers == {c[0] for c in M.FWD_CASES} | {c[0] for c in M.BWD_CASES}
+    assert len(names) >= 13
+
+
+def test_launch_log_starts_empty_and_resets():
+    capi.launch_log_reset()
+    assert capi.launch_log() == []

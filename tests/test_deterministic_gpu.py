@@ -1,16 +1,20 @@
 """Deterministic mode (ember_set_deterministic) of attention_bwd on the GPU.
 
-With the switch on, S > 128 stores each key block's dQ contribution into a
-partial slab and sums the slabs per row in ascending key order
-(attn_bwd_dq_reduce) instead of adding them into dQ with atomics.  Checked
-here, on contiguous and padded layouts, causal or not, every head dim, S
-from 65 (one key block with a tail) to 4096 (32 key blocks):
+With the switch on, the kernels that add dQ with atomics (S > 128, S > 64
+at D = 32) add each 16- or 32-row dQ tile's key-block contributions in a
+fixed order, highest key block first (ordered dQ: a counter per tile, O(S)
+scratch), instead of in arrival order.  Checked here, on contiguous and
+padded layouts, causal or not, every head dim, S from 65 (one key block with
+a tail) to 32768 (512 key blocks of 64):
 * dQ is bitwise identical over repeated launches, with default-mode
   launches in between (the default mode's atomics vary the order);
-* dK and dV are bitwise the default mode's (same kernels but for the dQ
-  store), and dQ agrees with the default mode's to fp32 rounding;
+* dK and dV are bitwise the default mode's (same kernels but for the order
+  of the dQ adds), and dQ agrees with the default mode's to fp32 rounding;
 * dQ, dK, dV agree with the CPU oracle at the north-star tolerance
-  (max-abs 2e-4 / rel 1e-3), and padding stays untouched;
+  (max-abs 2e-4 / rel 1e-3), or with float64 on sampled rows where the
+  oracle cannot reach, and padding stays untouched;
+* no wait for a tile's turn gave up (ember_deterministic_timeouts() == 0),
+  so every order above was the fixed one;
 * the Python front end (ember_amd.set_deterministic + attention_backward)
   takes the same path.
 S <= 64, and S <= 128 at D = 64 and 128 (attn_bwd_s128), have no atomics in
@@ -104,6 +108,8 @@ def test_deterministic_dq_is_reproducible_and_exact(B, H, S, D, causal, pads, hp
     for name, buf in zip(("dq", "dk", "dv"), bufs):
         assert np.count_nonzero(buf == G.SENTINEL) == p.in_tot - B * H * S * D, name
 
+    assert capi.deterministic_timeouts() == 0
+
     # The oracle on at most 4 heads (config 3's slice is 2).
     nh = min(H, 4)
     sl = (slice(0, 1), slice(0, nh))
@@ -148,3 +154,42 @@ def test_front_end_deterministic_backward():
     refs = oracle.attention_bwd(q[:1, :2], k[:1, :2], v[:1, :2], o_ref, lse_ref, d_o[:1, :2], True)
     for got, ref in zip(first, refs):
         np.testing.assert_allclose(got[:1, :2], ref, **TOL)
+
+
+@pytest.mark.parametrize("S,D,causal", [(32768, 64, True), (16384, 128, True), (8192, 64, False)])
+def test_deterministic_long_sequence(S, D, causal, deterministic):
+    """B=1 H=2 at up to S = 32768: O(S) scratch (the tile counters), so long
+    sequences run in deterministic mode as in the default mode.  dQ is
+    bitwise repeatable, dK and dV are bitwise the default mode's, and dQ
+    rows, dK and dV keys at tile edges and random positions agree with
+    float64 evaluations of the closed-form gradients from the given O and
+    LSE (P = exp(scale q.k - LSE), Delta = dO.O)."""
+    rng = np.random.default_rng(S + D)
+    q, k, v, d_o = (rng.standard_normal((1, 2, S, D), dtype=np.float32) for _ in range(4))
+    scale = G.scale_for(D)
+    o, lse = G.attention_fwd(q, k, v, causal)
+    dq1, dk1, dv1 = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    dq2, dk2, dv2 = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    assert capi.deterministic_timeouts() == 0
+    assert np.array_equal(dq1, dq2) and np.array_equal(dk1, dk2) and np.array_equal(dv1, dv2)
+    capi.set_deterministic(False)
+    _, dk0, dv0 = G.attention_bwd(q, k, v, o, lse, d_o, causal)
+    capi.set_deterministic(True)
+    assert np.array_equal(dk1, dk0) and np.array_equal(dv1, dv0)
+    picks = sorted({0, 1, 15, 16, 63, 64, 127, 128, S // 2, S - 65, S - 17, S - 1}
+                   | set(rng.choice(S, 8, replace=False).tolist()))
+    for h in range(2):
+        q64, k64, v64, g64 = (x[0, h].astype(np.float64) for x in (q, k, v, d_o))
+        lse64 = lse[0, h].astype(np.float64)
+        delta = (g64 * o[0, h].astype(np.float64)).sum(axis=1)
+        for i in picks:
+            nk = i + 1 if causal else S
+            p = np.exp(scale * (k64[:nk] @ q64[i]) - lse64[i])
+            ds = p * (v64[:nk] @ g64[i] - delta[i])
+            np.testing.assert_allclose(dq1[0, h, i], scale * (ds @ k64[:nk]), err_msg=f"dQ {h}/{i}", **TOL)
+        for j in picks:
+            i0 = j if causal else 0
+            p = np.exp(scale * (q64[i0:] @ k64[j]) - lse64[i0:])
+            ds = p * (g64[i0:] @ v64[j] - delta[i0:])
+            np.testing.assert_allclose(dv1[0, h, j], p @ g64[i0:], err_msg=f"dV {h}/{j}", **TOL)
+            np.testing.assert_allclose(dk1[0, h, j], scale * (ds @ q64[i0:]), err_msg=f"dK {h}/{j}", **TOL)

@@ -4,7 +4,8 @@ through the C ABI: dK and dV bit for bit, dQ (summed with atomics in a
 run-dependent order) within 1e-5, on consecutive calls of decreasing size;
 the largest accepted size (2^21 padded rows) moves no device memory; a larger
 call is rejected before any launch.  The medium call is also held to the
-north-star tolerance against the CPU oracle."""
+north-star tolerance against the CPU oracle.  In deterministic mode both
+entry points give the same bits for dQ as well."""
 
 import ctypes
 
@@ -107,6 +108,25 @@ def test_noalloc_matches_attention_bwd_on_consecutive_calls():
     capi.check(mid128.run("attention_bwd"), "attention_bwd")
     new = mid128.compare()
     assert np.array_equal(new[0], mid128.out["attention_bwd"][0].numpy())
+
+
+def test_noalloc_deterministic_matches_attention_bwd():
+    """Deterministic mode: the tile counters live in the same fixed array, and
+    both entry points add every dQ tile in the same fixed order, so dQ, dK
+    and dV are the same bits; two calls in a row, the second smaller."""
+    capi.set_deterministic(True)
+    try:
+        for B, H, S, D, causal, seed in ((2, 8, 1024, 64, True, 6), (1, 3, 300, 128, False, 7)):
+            case = _Case(B, H, S, D, causal, seed)
+            capi.check(case.run("attention_bwd_noalloc"), "attention_bwd_noalloc")
+            capi.check(case.run("attention_bwd"), "attention_bwd")
+            reg = [x.numpy() for x in case.out["attention_bwd"]]
+            new = [x.numpy() for x in case.out["attention_bwd_noalloc"]]
+            for name, a, b in zip(("dq", "dk", "dv"), new, reg):
+                assert np.array_equal(a, b), name
+        assert capi.deterministic_timeouts() == 0
+    finally:
+        capi.set_deterministic(False)
 
 
 def test_noalloc_rejects_more_rows_than_its_array():
