@@ -914,13 +914,233 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_split(FwdArgs a)
     }
 }
 
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// attn_fwd_split at 16 queries per workgroup, for launches with at most one
+// such workgroup per CU (config 1's B1 H4 S256: 64 workgroups against 32):
+// every product on v_mfma_f32_16x16x4f32, so a wave's 16 x 32 tile costs
+// half the matrix-core time of the 32 x 32 one and a query block spreads
+// over twice the CUs, with no exchange between workgroups.
+// 16 x 16 x 4 placement (lane l = n + 16 g): A[m][k] from lane m + 16k,
+// B[k][n] from lane n + 16k, C[m][n] in lane n + 16(m/4), register m % 4.
+//   S^T (keys x queries) = K . Q^T, per 16-key block: lane (n, g) supplies
+//     K[key n][D/4 g + s] and Q[query n][D/4 g + s] at k-step s (each lane
+//     group contracts a contiguous quarter of d);  C: lane (query n, g),
+//     register r <-> key 4g + r of the block.
+//   O^T (d x queries) += V^T . P^T, per 16-key block and k-step r: the
+//     B operand is P^T[key 4g + r][query n], i.e. register r of the S^T
+//     accumulator; the A operand of column block j is V[key 4g + r][E n + j]
+//     (E = D/16: lane n loads E consecutive floats of the row), so that
+//     output register r of block j in lane (n, g) is O[query n][E(4g + r) + j].
+// The online softmax, lazy rescaling and final merge are attn_fwd_split's.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 1) void attn_fwd_split16(FwdArgs a)
+{
+    constexpr int DQ = D / 4;   // k-steps of S per 16-key block
+    constexpr int E = D / 16;   // column blocks of O^T; floats of a V row per lane
+    __shared__ float part[kWaves * D * 16];  // O^T partials [w][d][query]
+    __shared__ float mst[kWaves * 16], lst[kWaves * 16];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+
+    const int nqb = a.nqb;  // 16-query blocks per head
+    const int bh = blockIdx.x / nqb;
+    const int qb = blockIdx.x - bh * nqb;
+    const int b = bh / a.H;
+    const int hh = bh - b * a.H;
+    const int S = a.S;
+    const int m0 = 16 * qb;
+    const int mq = m0 + n;
+    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
+
+    float qr[DQ];
+    {
+        const int mrow = mq < S ? mq : S - 1;
+        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + DQ * g;
+#pragma unroll
+        for (int s4 = 0; s4 < DQ; s4 += 4) {
+            const f32x4 t = *(const f32x4 *)(src + s4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qr[s4 + j] = t[j];
+        }
+    }
+
+    // A 32-key tile: K rows n0 + 16c + n (columns DQ g ..), V rows
+    // n0 + 16c + 4g + r (columns E n ..); rows past S clamped (masked).
+    float kr[2][DQ];
+    float vr[2][4][E];
+    auto load_tile = [&](int n0, float (&kd)[2][DQ], float (&vd)[2][4][E]) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int nk = min(n0 + 16 * c + n, S - 1);
+            const float *ks = a.k + in_base + (int64_t)nk * a.in_ss + DQ * g;
+#pragma unroll
+            for (int s4 = 0; s4 < DQ; s4 += 4) {
+                const f32x4 t = *(const f32x4 *)(ks + s4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kd[c][s4 + j] = t[j];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int nv = min(n0 + 16 * c + 4 * g + r, S - 1);
+                const float *vs = a.v + in_base + (int64_t)nv * a.in_ss + E * n;
+#pragma unroll
+                for (int j4 = 0; j4 < E; j4 += 4) {
+                    const f32x4 t = *(const f32x4 *)(vs + j4);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) vd[c][r][j4 + j] = t[j];
+                }
+            }
+        }
+    };
+
+    f32x4 oacc[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mrun = -INFINITY, lrun = 0.0f;
+
+    const int kend = CAUSAL ? min(S, m0 + 16) : S;
+    const int ntiles = (kend + 31) / 32;
+    int t = w;
+    if (t < ntiles) load_tile(32 * t, kr, vr);
+    for (; t < ntiles; t += kWaves) {
+        const int n0 = 32 * t;
+        float kn[2][DQ];
+        float vn[2][4][E];
+        const bool more = t + kWaves < ntiles;
+        if (more) load_tile(n0 + 32 * kWaves, kn, vn);
+
+        f32x4 sacc[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            sacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < DQ; ++s) sacc[c] = mfma16(kr[c][s], qr[s], sacc[c]);
+        }
+        if (n0 + 32 > S || (CAUSAL && n0 + 31 > m0)) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = n0 + 16 * c + 4 * g + r;
+                    const bool vis = (key < S) & (!CAUSAL | (key <= mq));
+                    sacc[c][r] = vis ? sacc[c][r] : -INFINITY;
+                }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[c][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float tm2 = tmax * a.c;
+        if (__ballot(tm2 > mrun + 8.0f) != 0) {
+            const float mnew = fmaxf(mrun, tm2);
+            const float alpha = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
+            mrun = mnew;
+            lrun *= alpha;
+#pragma unroll
+            for (int j = 0; j < E; ++j) oacc[j] *= alpha;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float sv = sacc[c][r];
+                const float p = sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv, a.c, -mrun));
+                sacc[c][r] = p;
+                lrun += p;
+            }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int j = 0; j < E; ++j) oacc[j] = mfma16(vr[c][r][j], sacc[c][r], oacc[j]);
+        if (more) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+#pragma unroll
+                for (int s = 0; s < DQ; ++s) kr[c][s] = kn[c][s];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int j = 0; j < E; ++j) vr[c][r][j] = vn[c][r][j];
+            }
+        }
+    }
+
+    // Publish this wave's state: m (scaled log2 units), l summed over the
+    // four lane groups, O^T.
+    float ltot = lrun + __shfl_xor(lrun, 16);
+    ltot += __shfl_xor(ltot, 32);
+    if (g == 0) {
+        mst[w * 16 + n] = mrun;
+        lst[w * 16 + n] = ltot;
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[(w * D + E * (4 * g + r) + j) * 16 + n] = oacc[j][r];
+    __syncthreads();
+
+    // Merge: thread (w, g) writes d in [E (4w + g), E (4w + g) + E) of query n.
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) M = fmaxf(M, mst[v * 16 + n]);
+    float f[kWaves], L = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) {
+        const float mv = mst[v * 16 + n];
+        f[v] = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - M);
+        L += f[v] * lst[v * 16 + n];
+    }
+    if (mq < S) {
+        const float inv = 1.0f / L;
+        const int d0 = E * (4 * w + g);
+        float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss + d0;
+#pragma unroll
+        for (int d4 = 0; d4 < E; d4 += 4) {
+            f32x4 o4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int v = 0; v < kWaves; ++v) acc += f[v] * part[(v * D + d0 + d4 + j) * 16 + n];
+                o4[j] = acc * inv;
+            }
+            *(f32x4 *)(orow + d4) = o4;
+        }
+        if (w == 0 && g == 0) a.lse[(int64_t)bh * S + mq] = (M + log2f(L)) * kLn2;
+    }
+}
+
 template <int D, bool CAUSAL>
 int launch_fwd(FwdArgs args, int64_t nbh)
 {
     // A launch that would leave most CUs idle (and is longer than the
-    // packed short-sequence case) splits the keys across waves instead.
+    // packed short-sequence case) splits the keys across waves instead, at
+    // 16 queries per workgroup where that still fits one workgroup per CU.
     const int64_t regular = (args.S + kBr - 1) / kBr * nbh;
     if (args.S > 64 && regular * 4 <= 256) {
+        if constexpr (D >= 64) {
+            const int64_t nqb16 = (args.S + 15) / 16;
+            const int ncu = device_cu_count();
+            if (nqb16 * nbh <= (ncu > 0 ? ncu : 256)) {
+                args.nqb = (int)nqb16;
+                hipLaunchKernelGGL((attn_fwd_split16<D, CAUSAL>), dim3((unsigned)(args.nqb * nbh)),
+                                   dim3(kThreads), 0, 0, args);
+                return launch_ok("attn_fwd_split16") ? EMBER_OK : EMBER_ERR_DEVICE;
+            }
+        }
         args.nqb = (args.S + 31) / 32;
         hipLaunchKernelGGL((attn_fwd_split<D, CAUSAL>), dim3((unsigned)(args.nqb * nbh)), dim3(kThreads),
                            0, 0, args);

@@ -21,10 +21,10 @@ backward (dQ, dK, dV, with O and LSE passed in unchanged):
     <= c_h as well (with O and LSE fixed, key j's gradient reads only row j
     of K and V).  Kernels whose dQ is added with atomics run this check in
     deterministic mode, whose per-row sum order is fixed.
-Two tilings (forward): the same head through attn_fwd_split (alone) and
-through attn_fwd_kernel or attn_fwd_wave_pair (among 65 heads) agrees within
-the north-star tolerance and with the CPU oracle, and both pass the cutoff
-check above.  Every launch's first and last head are also held to the oracle
+Two tilings (forward): the same head through a split-key kernel (in a
+small launch) and through attn_fwd_kernel or attn_fwd_wave_pair (among 65
+heads) agrees within the north-star tolerance and with the CPU oracle, and
+both pass the cutoff check above.  Every launch's first and last head are also held to the oracle
 at the north-star tolerance.
 
 The slot these kernels fill is the reference's src/tensor/operators.h:20-27;
@@ -110,10 +110,13 @@ def _oracle_heads(q, k, v, o, lse, heads):
 
 # (kernel, B, H, S, D): each shape reaches the named forward kernel.
 FWD_CASES = [
-    ("attn_fwd_split", 1, 1, 300, 128),        # <= 64 one-head workgroups
-    ("attn_fwd_split", 1, 2, 300, 64),
-    ("attn_fwd_split", 1, 4, 1024, 64),
-    ("attn_fwd_split", 1, 2, 129, 32),
+    ("attn_fwd_split16", 1, 1, 300, 128),      # <= 256 16-query workgroups
+    ("attn_fwd_split16", 1, 2, 300, 64),
+    ("attn_fwd_split16", 1, 4, 1024, 64),
+    ("attn_fwd_split16", 1, 4, 256, 64),       # config 1's shape
+    ("attn_fwd_split", 1, 5, 1024, 64),        # <= 64 one-head 128-query blocks, > 256 of 16
+    ("attn_fwd_split", 1, 3, 2048, 128),
+    ("attn_fwd_split", 1, 2, 129, 32),         # D = 32
     ("attn_fwd_kernel", 1, 65, 129, 128),      # 128-query workgroups
     ("attn_fwd_kernel", 1, 65, 300, 64),
     ("attn_fwd_kernel", 1, 33, 1024, 128),
@@ -159,35 +162,40 @@ def test_forward_mask_is_bit_exact(kernel, B, H, S, D):
     _oracle_heads(q, k, v, o, lse, (0, B * H - 1))
 
 
-@pytest.mark.parametrize("S,D,other", [(300, 128, "attn_fwd_kernel"), (1024, 64, "attn_fwd_kernel"),
-                                       (128, 64, "attn_fwd_wave_pair"), (100, 128, "attn_fwd_wave_pair")])
-def test_two_tilings_same_mask(S, D, other):
-    """One head through attn_fwd_split (32-query blocks, four waves over
-    interleaved 32-key tiles) and through a second kernel (128-query blocks
-    over 64-key tiles, or one wave per pair of 32-query blocks) as head 7 of
-    65: both pass the cutoff check with the same cutoffs for that head, and
-    agree with the oracle and with each other within the north-star
-    tolerance."""
+@pytest.mark.parametrize("S,D,H1,alone,other", [
+    (300, 128, 1, "attn_fwd_split16", "attn_fwd_kernel"),
+    (1024, 64, 5, "attn_fwd_split", "attn_fwd_kernel"),
+    (128, 64, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
+    (100, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
+    (2048, 128, 3, "attn_fwd_split", "attn_fwd_kernel"),
+])
+def test_two_tilings_same_mask(S, D, H1, alone, other):
+    """One head through a split-key kernel (16 or 32 queries per workgroup,
+    four waves over interleaved 32-key tiles; as head 0 of H1) and through a
+    second kernel (128-query blocks over 64-key tiles, or one wave per pair of
+    32-query blocks) as head 7 of 65: both pass the cutoff check with the same
+    cutoffs for that head, and agree with the oracle and with each other
+    within the north-star tolerance."""
     rng = np.random.default_rng(S + D)
-    q1, k1, v1 = (_rand((1, 1, S, D), rng) for _ in range(3))
+    q1, k1, v1 = (_rand((1, H1, S, D), rng) for _ in range(3))
     qs, ks, vs = (_rand((1, 65, S, D), rng) for _ in range(3))
     for big, one in ((qs, q1), (ks, k1), (vs, v1)):
         big[0, 7] = one[0, 0]
-    one_rounds = _cutoff_rounds(1, S, S)
+    one_rounds = _cutoff_rounds(H1, S, S)
     many_rounds = []
     for r, cut1 in enumerate(one_rounds):
         cut = _cutoff_rounds(65, S, S + r)[0]
         cut[7] = cut1[0]
         many_rounds.append(cut)
-    G.say(f"two tilings S={S} D={D}: attn_fwd_split")
-    o1, lse1 = _forward_cutoff_check(q1, k1, v1, one_rounds, "attn_fwd_split", S)
+    G.say(f"two tilings S={S} D={D}: {alone}")
+    o1, lse1 = _forward_cutoff_check(q1, k1, v1, one_rounds, alone, S)
     G.say(f"two tilings S={S} D={D}: {other}")
     o65, lse65 = _forward_cutoff_check(qs, ks, vs, many_rounds, other, S + 1)
     np.testing.assert_allclose(o65[0, 7], o1[0, 0], **TOL)
     np.testing.assert_allclose(lse65[0, 7], lse1[0, 0], **TOL)
-    o_ref, lse_ref = oracle.attention_fwd(q1, k1, v1, True)
-    np.testing.assert_allclose(o1, o_ref, **TOL)
-    np.testing.assert_allclose(lse1, lse_ref, **TOL)
+    o_ref, lse_ref = oracle.attention_fwd(q1[:, :1], k1[:, :1], v1[:, :1], True)
+    np.testing.assert_allclose(o1[:, :1], o_ref, **TOL)
+    np.testing.assert_allclose(lse1[:, :1], lse_ref, **TOL)
     np.testing.assert_allclose(o65[:, 7:8], o_ref, **TOL)
     np.testing.assert_allclose(lse65[:, 7:8], lse_ref, **TOL)
 
