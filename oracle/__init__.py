@@ -45,6 +45,10 @@ def build(reference_root: str = "/root/reference") -> None:
     subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle.so"], check=True)
     if os.path.isdir(os.path.join(reference_root, "src", "tensor")):
         subprocess.run(["make", "-s", "-B", "-C", _HERE, "ref", f"REF={reference_root}"], check=True)
+        # The reference's own bindings linked against libember_amd.so (the
+        # executed drop-in check of tests/test_reference_binding_gpu.py).
+        if os.path.isdir(os.path.join(reference_root, "src", "random")):
+            subprocess.run(["make", "-s", "-B", "-C", _HERE, "link-check", f"REF={reference_root}"], check=True)
 
 
 def lib() -> C.CDLL:
