@@ -1123,6 +1123,174 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_split16(FwdArgs a)
     }
 }
 
+// 64 < S <= 128 at D = 64 and 128 over many heads: one persistent
+// workgroup of 8 waves per CU walks whole heads.  A head's K and V (at most
+// 128 rows) are staged in LDS once, from registers that were filled with
+// that head's rows while the previous head was multiplied (4 threads per
+// row, coalesced), so each of Q, K, V is read from HBM once.  A wave owns
+// one 16-query chunk; causally the hardware's placement of waves w and
+// w + 4 on one SIMD gives SIMD j the chunks j and nch - 1 - j, which see
+// nch + 1 key chunks together (9 at S = 128 on every SIMD), with no
+// lockstep between waves (one barrier pair per head, around the staging).
+// The products are attn_fwd_split16's (v_mfma_f32_16x16x4f32; placement
+// documented there) with K and V read from LDS: per key chunk,
+// S^T = K . Q^T (16 keys x 16 queries), the online softmax with lazy
+// rescaling, O^T += V^T . P^T; masked work is cut at 16 x 16.
+template <int D>
+struct HeadTile {
+    static constexpr int KSTR = D + 4;  // padded K row
+    static constexpr int PER = D / 4;   // floats of a K or V row per staging thread
+};
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(512, D == 64 ? 2 : 1) void attn_fwd_head(FwdArgs a)
+{
+    typedef HeadTile<D> T;
+    constexpr int DQ = D / 4;  // k-steps of S per key chunk
+    constexpr int E = D / 16;  // column blocks of O^T; floats of a V row per lane
+    constexpr int KSTR = T::KSTR, PER = T::PER;
+    __shared__ float Ks[128 * KSTR];
+    __shared__ float Vs[128 * D];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int S = a.S;
+    const int nch = (S + 15) >> 4;
+    // This wave's query chunk.  Waves w and w + 4 share a SIMD.  Causal:
+    // SIMD j < ceil(nch / 2) takes chunks j and nch - 1 - j, which see
+    // nch + 1 key chunks together.  Non-causal: chunk w.
+    const int sj = w & 3, second = w >> 2;
+    int c;
+    bool active;
+    if (CAUSAL) {
+        c = second ? nch - 1 - sj : sj;
+        active = 2 * sj < nch && (!second || nch - 1 - sj > sj);
+    } else {
+        c = w;
+        active = w < nch;
+    }
+    const int m0 = 16 * c;
+    const int mq = m0 + n;
+    const int srow = tid >> 2, spart = tid & 3;  // staging: K / V row and quarter
+    const int srow_c = min(srow, S - 1);          // rows past S re-read row S - 1 (masked)
+    const int qrow_c = min(mq, S - 1);
+
+    f32x4 kp[PER / 4], vp[PER / 4], qp[DQ / 4];
+    auto prefetch = [&](int bh) {
+        const int b = bh / a.H;
+        const int64_t base = (int64_t)b * a.in_sb + (int64_t)(bh - b * a.H) * a.in_sh;
+        const float *ks = a.k + base + (int64_t)srow_c * a.in_ss + PER * spart;
+        const float *vs = a.v + base + (int64_t)srow_c * a.in_ss + PER * spart;
+#pragma unroll
+        for (int i = 0; i < PER / 4; ++i) {
+            kp[i] = *(const f32x4 *)(ks + 4 * i);
+            vp[i] = *(const f32x4 *)(vs + 4 * i);
+        }
+        if (active) {
+            const float *qs = a.q + base + (int64_t)qrow_c * a.in_ss + DQ * g;
+#pragma unroll
+            for (int i = 0; i < DQ / 4; ++i) qp[i] = *(const f32x4 *)(qs + 4 * i);
+        }
+    };
+
+    const int nbh = a.nbh;
+    int bh = blockIdx.x;
+    if (bh < nbh) prefetch(bh);
+    for (; bh < nbh; bh += gridDim.x) {
+        __syncthreads();  // the previous head's products are done with Ks, Vs
+#pragma unroll
+        for (int i = 0; i < PER / 4; ++i) {
+            *(f32x4 *)&Ks[srow * KSTR + PER * spart + 4 * i] = kp[i];
+            *(f32x4 *)&Vs[srow * D + PER * spart + 4 * i] = vp[i];
+        }
+        float qr[DQ];
+#pragma unroll
+        for (int i = 0; i < DQ / 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qr[4 * i + j] = qp[i][j];
+        if (bh + (int)gridDim.x < nbh) prefetch(bh + gridDim.x);
+        __syncthreads();
+        if (!active) continue;
+
+        f32x4 oacc[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float mrun = -INFINITY, lrun = 0.0f;
+        const int kc_end = CAUSAL ? c : nch - 1;
+        for (int kc = 0; kc <= kc_end; ++kc) {
+            const int k0 = 16 * kc;
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+            const float *krow = &Ks[(k0 + n) * KSTR + DQ * g];
+#pragma unroll
+            for (int s4 = 0; s4 < DQ; s4 += 4) {
+                const f32x4 kf = *(const f32x4 *)(krow + s4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sacc = mfma16(kf[j], qr[s4 + j], sacc);
+            }
+            if ((CAUSAL && kc == c) || k0 + 16 > S) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 4 * g + r;
+                    const bool vis = (key < S) & (!CAUSAL | (key <= mq));
+                    sacc[r] = vis ? sacc[r] : -INFINITY;
+                }
+            }
+            float tmax = fmaxf(fmaxf(sacc[0], sacc[1]), fmaxf(sacc[2], sacc[3]));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float tm2 = tmax * a.c;
+            if (__ballot(tm2 > mrun + 8.0f) != 0) {
+                const float mnew = fmaxf(mrun, tm2);
+                const float alpha = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
+                mrun = mnew;
+                lrun *= alpha;
+#pragma unroll
+                for (int j = 0; j < E; ++j) oacc[j] *= alpha;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float sv = sacc[r];
+                const float p = sv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sv, a.c, -mrun));
+                sacc[r] = p;
+                lrun += p;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float *vrow = &Vs[(k0 + 4 * g + r) * D + E * n];
+#pragma unroll
+                for (int j4 = 0; j4 < E; j4 += 4) {
+                    const f32x4 vf = *(const f32x4 *)(vrow + j4);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) oacc[j4 + j] = mfma16(vf[j], sacc[r], oacc[j4 + j]);
+                }
+            }
+        }
+
+        float ltot = lrun + __shfl_xor(lrun, 16);
+        ltot += __shfl_xor(ltot, 32);
+        if (mq < S) {
+            const int b = bh / a.H;
+            const int hh = bh - b * a.H;
+            const float inv = 1.0f / ltot;
+            float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int j4 = 0; j4 < E; j4 += 4) {
+                    f32x4 o4;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) o4[j] = oacc[j4 + j][r] * inv;
+                    *(f32x4 *)(orow + E * (4 * g + r) + j4) = o4;
+                }
+            }
+            if (g == 0) a.lse[(int64_t)bh * S + mq] = (mrun + log2f(ltot)) * kLn2;
+        }
+    }
+}
+
 template <int D, bool CAUSAL>
 int launch_fwd(FwdArgs args, int64_t nbh)
 {
@@ -1145,6 +1313,23 @@ int launch_fwd(FwdArgs args, int64_t nbh)
         hipLaunchKernelGGL((attn_fwd_split<D, CAUSAL>), dim3((unsigned)(args.nqb * nbh)), dim3(kThreads),
                            0, 0, args);
         return launch_ok("attn_fwd_split") ? EMBER_OK : EMBER_ERR_DEVICE;
+    }
+    // D = 64, causal 64 < S <= 128 and non-causal 64 < S <= 80: persistent
+    // workgroups over whole heads (K, V read once).  Measured at 2^20 query
+    // rows against the paired-wave kernel: causal S = 128 3.71 -> 4.30 TB/s,
+    // S = 112 3.36 -> 4.26, S = 80 3.69 -> 4.03, S = 96 4.12 -> 4.15;
+    // non-causal S = 72 2.62 -> 3.19, S = 80 2.81 -> 3.55; non-causal S = 96
+    // (3.06 against 3.21) and S = 128 (3.06 against the workgroup kernel's
+    // 3.29) keep the kernels below.  At D = 128 the staged head fills a CU's
+    // LDS alone and measured 14 % slower than the paired waves.
+    if constexpr (D == 64) {
+        if (args.S > 64 && (CAUSAL ? args.S <= 128 : args.S <= 80)) {
+            const int ncu = device_cu_count();
+            const int64_t slots = (int64_t)(ncu > 0 ? ncu : 256) * (D == 64 ? 2 : 1);
+            hipLaunchKernelGGL((attn_fwd_head<D, CAUSAL>), dim3((unsigned)(nbh < slots ? nbh : slots)), dim3(512),
+                               0, 0, args);
+            return launch_ok("attn_fwd_head") ? EMBER_OK : EMBER_ERR_DEVICE;
+        }
     }
     // 64 < S <= 96, and causal S <= 128 (D >= 64): one wave per pair of
     // 32-query blocks.  The 128-query workgroups leave a quarter or more of

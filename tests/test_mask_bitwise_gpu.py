@@ -22,7 +22,7 @@ backward (dQ, dK, dV, with O and LSE passed in unchanged):
     of K and V).  Kernels whose dQ is added with atomics run this check in
     deterministic mode, whose per-row sum order is fixed.
 Two tilings (forward): the same head through a split-key kernel (in a
-small launch) and through attn_fwd_kernel or attn_fwd_wave_pair (among 65
+small launch) and through attn_fwd_kernel, attn_fwd_head or attn_fwd_wave_pair (among 65
 heads) agrees within the north-star tolerance and with the CPU oracle, and
 both pass the cutoff check above.  Every launch's first and last head are also held to the oracle
 at the north-star tolerance.
@@ -122,9 +122,13 @@ FWD_CASES = [
     ("attn_fwd_kernel", 1, 33, 1024, 128),
     ("attn_fwd_kernel", 1, 40, 1024, 64),
     ("attn_fwd_kernel", 1, 65, 200, 32),
-    ("attn_fwd_wave_pair", 1, 65, 80, 64),     # one wave per pair of query blocks
+    ("attn_fwd_head", 1, 65, 128, 64),         # persistent whole-head workgroups, D = 64
+    ("attn_fwd_head", 1, 300, 80, 64),         # more heads than CUs: each workgroup walks several
+    ("attn_fwd_head", 1, 70, 113, 64),
+    ("attn_fwd_head", 1, 65, 97, 64),
+    ("attn_fwd_wave_pair", 1, 65, 80, 128),    # one wave per pair of query blocks
     ("attn_fwd_wave_pair", 1, 65, 128, 128),
-    ("attn_fwd_wave_pair", 1, 70, 113, 64),
+    ("attn_fwd_wave_pair", 1, 70, 113, 128),
     ("attn_fwd_wave", 1, 65, 64, 128),         # one wave per query block, S <= 64
     ("attn_fwd_wave", 1, 65, 40, 64),
     ("attn_fwd_wave", 1, 9, 17, 128),
@@ -165,15 +169,17 @@ def test_forward_mask_is_bit_exact(kernel, B, H, S, D):
 @pytest.mark.parametrize("S,D,H1,alone,other", [
     (300, 128, 1, "attn_fwd_split16", "attn_fwd_kernel"),
     (1024, 64, 5, "attn_fwd_split", "attn_fwd_kernel"),
-    (128, 64, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
+    (128, 64, 1, "attn_fwd_split16", "attn_fwd_head"),
+    (96, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
     (100, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
     (2048, 128, 3, "attn_fwd_split", "attn_fwd_kernel"),
 ])
 def test_two_tilings_same_mask(S, D, H1, alone, other):
     """One head through a split-key kernel (16 or 32 queries per workgroup,
     four waves over interleaved 32-key tiles; as head 0 of H1) and through a
-    second kernel (128-query blocks over 64-key tiles, or one wave per pair of
-    32-query blocks) as head 7 of 65: both pass the cutoff check with the same
+    second kernel (128-query blocks over 64-key tiles, whole heads staged in
+    LDS with 16-query chunks, or one wave per pair of 32-query blocks) as
+    head 7 of 65: both pass the cutoff check with the same
     cutoffs for that head, and agree with the oracle and with each other
     within the north-star tolerance."""
     rng = np.random.default_rng(S + D)
