@@ -263,15 +263,14 @@ def _timed(ev, fn, reps, settle_s=0.15):
 
 def short_s_study(L, ev, copy_probe_mb, reps=5):
     """Attention where it is HBM-bound: the forward at S = 32, 64, 128 and
-    D = 128, causal, 2^20 query rows per tensor (the shapes `secondary`
+    D = 64, 128, causal, 2^20 query rows per tensor (the shapes `secondary`
     reports), achieved bandwidth over the algorithmic bytes 16*B*H*S*D +
-    4*B*H*S; then the backward at S = 32, 64, 128 (D = 64, 128).  With
-    copy_probe_mb, one negate_tensor pass over that many MiB follows (known
-    bytes for scaling the traffic counters)."""
+    4*B*H*S; then the backward at the same shapes.  With copy_probe_mb, one
+    negate_tensor pass over that many MiB follows (known bytes for scaling
+    the traffic counters)."""
     out = {}
     rng = np.random.default_rng(7)
-    D = 128
-    for S in (32, 64, 128):
+    for S, D in ((32, 64), (32, 128), (64, 64), (64, 128), (128, 64), (128, 128)):
         B, H = (1 << 20) // S // 64, 64
         n = B * H * S * D
         q, k, v = (DeviceArray((n,), rng.standard_normal(n, dtype=np.float32)) for _ in range(3))
@@ -282,7 +281,7 @@ def short_s_study(L, ev, copy_probe_mb, reps=5):
                                                 *st, *st), reps)
         capi.check(what=f"short-S forward S={S}")
         byts = 16 * n + 4 * B * H * S
-        out[f"short_s{S}_fwd"] = {"shape": f"B{B} H{H} S{S} D{D} causal=True", "fwd_ms": round(ms, 4),
+        out[f"short_s{S}_d{D}_fwd"] = {"shape": f"B{B} H{H} S{S} D{D} causal=True", "fwd_ms": round(ms, 4),
                                   "algorithmic_bytes": byts, "fwd_hbm_gbs": round(byts / ms / 1e6, 1),
                                   "frac_of_hbm_peak": round(byts / ms / 1e6 / PEAK_HBM_GBS, 4)}
         del q, k, v, o, lse
@@ -387,6 +386,8 @@ def secondary(L, ev):
         fwd_ms = _timed(ev, f, reps)
         rec = {"shape": f"B{B} H{H} S{S} D{D} causal={causal}", "fwd_ms": round(fwd_ms, 4),
                "fwd_tflops": round(fwd_fl / fwd_ms / 1e9, 2)}
+        if fwd_ms < 0.1:  # microsecond launches: four decimals of a millisecond hide them
+            rec["fwd_us"] = round(fwd_ms * 1e3, 2)
         if bwd:
             b = lambda: L.attention_bwd(q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, g.ptr, dq.ptr,  # noqa: E731
                                         dk.ptr, dv.ptr, B, H, S, D, sc, int(causal), *st, *st)
