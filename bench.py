@@ -238,13 +238,17 @@ def cpu_baseline(S, D, threads, inputs, outputs):
 
 
 def _timed(ev, fn, reps, settle_s=0.15):
-    """Average ms of fn() over reps launches, HIP events on the null stream.
+    """Average ms of fn() over reps back-to-back launches: one HIP event on
+    the null stream before the first and one after the last.
 
     fn() first runs back to back for settle_s seconds: after the host-side
     set-up between measurements the GPU sits idle and its engine clock drops,
     and it takes some tens of milliseconds of load to come back up (one
     warm-up launch before ten 1 ms GEMMs measured 126 against 147 TFLOP/s
-    after 50)."""
+    after 50).  An event recorded between every two launches would add its
+    own cost to each (a 64-element negate_tensor: 6.4 us per call timed that
+    way, 2.6-3.0 us back to back), which matters only for microsecond
+    launches such as config 1's forward."""
     L = capi.lib()
     t0 = time.perf_counter()
     fn()
@@ -253,12 +257,12 @@ def _timed(ev, fn, reps, settle_s=0.15):
         for _ in range(4):
             fn()
         L.sync_device()
-    marks = ev.create(reps + 1)
+    marks = ev.create(2)
     ev.record(marks[0])
-    for i in range(reps):
+    for _ in range(reps):
         fn()
-        ev.record(marks[i + 1])
-    return sum(ev.elapsed_ms(marks[i], marks[i + 1]) for i in range(reps)) / reps
+    ev.record(marks[1])
+    return ev.elapsed_ms(marks[0], marks[1]) / reps
 
 
 def short_s_study(L, ev, copy_probe_mb, reps=5):

@@ -936,13 +936,13 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c)
 //     (E = D/16: lane n loads E consecutive floats of the row), so that
 //     output register r of block j in lane (n, g) is O[query n][E(4g + r) + j].
 // The online softmax, lazy rescaling and final merge are attn_fwd_split's.
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 1) void attn_fwd_split16(FwdArgs a)
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void attn_fwd_split16(FwdArgs a)
 {
     constexpr int DQ = D / 4;   // k-steps of S per 16-key block
     constexpr int E = D / 16;   // column blocks of O^T; floats of a V row per lane
-    __shared__ float part[kWaves * D * 16];  // O^T partials [w][d][query]
-    __shared__ float mst[kWaves * 16], lst[kWaves * 16];
+    __shared__ float part[NW * D * 16];  // O^T partials [w][d][query]
+    __shared__ float mst[NW * 16], lst[NW * 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1010,12 +1010,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_split16(FwdArgs a)
     const int ntiles = (kend + 31) / 32;
     int t = w;
     if (t < ntiles) load_tile(32 * t, kr, vr);
-    for (; t < ntiles; t += kWaves) {
+    for (; t < ntiles; t += NW) {
         const int n0 = 32 * t;
         float kn[2][DQ];
         float vn[2][4][E];
-        const bool more = t + kWaves < ntiles;
-        if (more) load_tile(n0 + 32 * kWaves, kn, vn);
+        const bool more = t + NW < ntiles;
+        if (more) load_tile(n0 + 32 * NW, kn, vn);
 
         f32x4 sacc[2];
 #pragma unroll
@@ -1092,32 +1092,36 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_split16(FwdArgs a)
         for (int r = 0; r < 4; ++r) part[(w * D + E * (4 * g + r) + j) * 16 + n] = oacc[j][r];
     __syncthreads();
 
-    // Merge: thread (w, g) writes d in [E (4w + g), E (4w + g) + E) of query n.
+    // Merge: thread (w, g) writes d in [DPT (4w + g), DPT (4w + g) + DPT)
+    // of query n.
+    constexpr int DPT = D / (4 * NW);
+    static_assert(DPT == 2 || DPT % 4 == 0, "merge stores are 8 or 16 bytes");
     float M = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) M = fmaxf(M, mst[v * 16 + n]);
-    float f[kWaves], L = 0.0f;
+    for (int v = 0; v < NW; ++v) M = fmaxf(M, mst[v * 16 + n]);
+    float f[NW], L = 0.0f;
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) {
+    for (int v = 0; v < NW; ++v) {
         const float mv = mst[v * 16 + n];
         f[v] = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - M);
         L += f[v] * lst[v * 16 + n];
     }
     if (mq < S) {
         const float inv = 1.0f / L;
-        const int d0 = E * (4 * w + g);
+        const int d0 = DPT * (4 * w + g);
         float *orow = a.o + (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh + (int64_t)mq * a.out_ss + d0;
+        constexpr int VW = DPT == 2 ? 2 : 4;
 #pragma unroll
-        for (int d4 = 0; d4 < E; d4 += 4) {
-            f32x4 o4;
+        for (int d4 = 0; d4 < DPT; d4 += VW) {
+            typename VecN<VW>::T ov;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < VW; ++j) {
                 float acc = 0.0f;
 #pragma unroll
-                for (int v = 0; v < kWaves; ++v) acc += f[v] * part[(v * D + d0 + d4 + j) * 16 + n];
-                o4[j] = acc * inv;
+                for (int v = 0; v < NW; ++v) acc += f[v] * part[(v * D + d0 + d4 + j) * 16 + n];
+                ov[j] = acc * inv;
             }
-            *(f32x4 *)(orow + d4) = o4;
+            *(typename VecN<VW>::T *)(orow + d4) = ov;
         }
         if (w == 0 && g == 0) a.lse[(int64_t)bh * S + mq] = (M + log2f(L)) * kLn2;
     }
@@ -1304,7 +1308,16 @@ int launch_fwd(FwdArgs args, int64_t nbh)
             const int ncu = device_cu_count();
             if (nqb16 * nbh <= (ncu > 0 ? ncu : 256)) {
                 args.nqb = (int)nqb16;
-                hipLaunchKernelGGL((attn_fwd_split16<D, CAUSAL>), dim3((unsigned)(args.nqb * nbh)),
+                // Eight waves (one 32-key tile each at config 1's S = 256)
+                // where a D = 64 wave would otherwise walk two or more tiles.
+                if constexpr (D == 64) {
+                    if (args.S > 4 * 32) {
+                        hipLaunchKernelGGL((attn_fwd_split16<D, CAUSAL, 8>), dim3((unsigned)(args.nqb * nbh)),
+                                           dim3(512), 0, 0, args);
+                        return launch_ok("attn_fwd_split16_w8") ? EMBER_OK : EMBER_ERR_DEVICE;
+                    }
+                }
+                hipLaunchKernelGGL((attn_fwd_split16<D, CAUSAL, 4>), dim3((unsigned)(args.nqb * nbh)),
                                    dim3(kThreads), 0, 0, args);
                 return launch_ok("attn_fwd_split16") ? EMBER_OK : EMBER_ERR_DEVICE;
             }

@@ -110,10 +110,13 @@ def _oracle_heads(q, k, v, o, lse, heads):
 
 # (kernel, B, H, S, D): each shape reaches the named forward kernel.
 FWD_CASES = [
-    ("attn_fwd_split16", 1, 1, 300, 128),      # <= 256 16-query workgroups
-    ("attn_fwd_split16", 1, 2, 300, 64),
-    ("attn_fwd_split16", 1, 4, 1024, 64),
-    ("attn_fwd_split16", 1, 4, 256, 64),       # config 1's shape
+    ("attn_fwd_split16", 1, 1, 300, 128),      # <= 256 16-query workgroups, 4 waves
+    ("attn_fwd_split16", 1, 4, 128, 64),
+    ("attn_fwd_split16", 1, 3, 100, 64),
+    ("attn_fwd_split16_w8", 1, 2, 300, 64),    # 8 waves (D = 64, S > 128)
+    ("attn_fwd_split16_w8", 1, 4, 1024, 64),
+    ("attn_fwd_split16_w8", 1, 4, 256, 64),    # config 1's shape
+    ("attn_fwd_split16_w8", 1, 1, 4096, 64),   # 32 tiles per wave
     ("attn_fwd_split", 1, 5, 1024, 64),        # <= 64 one-head 128-query blocks, > 256 of 16
     ("attn_fwd_split", 1, 3, 2048, 128),
     ("attn_fwd_split", 1, 2, 129, 32),         # D = 32
@@ -169,6 +172,7 @@ def test_forward_mask_is_bit_exact(kernel, B, H, S, D):
 @pytest.mark.parametrize("S,D,H1,alone,other", [
     (300, 128, 1, "attn_fwd_split16", "attn_fwd_kernel"),
     (1024, 64, 5, "attn_fwd_split", "attn_fwd_kernel"),
+    (1024, 64, 1, "attn_fwd_split16_w8", "attn_fwd_kernel"),
     (128, 64, 1, "attn_fwd_split16", "attn_fwd_head"),
     (96, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
     (100, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
