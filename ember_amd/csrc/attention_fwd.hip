@@ -775,26 +775,29 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_split(FwdArgs a)
     float qr[DH];
     {
         const int mrow = mq < S ? mq : S - 1;
-        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + h32 * DH;
+        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + 4 * h32;
 #pragma unroll
         for (int kk = 0; kk < DH; kk += 4) {
-            const f32x4 t = *(const f32x4 *)(src + kk);
+            const f32x4 t = *(const f32x4 *)(src + 2 * kk);
 #pragma unroll
             for (int j = 0; j < 4; ++j) qr[kk + j] = t[j];
         }
     }
 
-    // K operand: lane holds K[n0 + l32][h32*DH + kk]; V operand for k-step i:
+    // K operand: lane holds K[n0 + l32][d] for k-step kk, with
+    // d = 8 (kk / 4) + 4 h32 + kk % 4 (Q^T likewise), so that the two lanes
+    // of a row read 32 contiguous bytes per load (32 cache lines per load
+    // instruction rather than 64); V operand for k-step i:
     // V[n0 + acc_row(i, h32)][DB*l32 .. +DB).  Rows past S are clamped
     // (their scores are masked).
     float kr[DH];
     VT vr[16];
     auto load_tile = [&](int n0, float (&kd)[DH], VT (&vd)[16]) {
         const int nk = n0 + l32 < S ? n0 + l32 : S - 1;
-        const float *ks = a.k + in_base + (int64_t)nk * a.in_ss + h32 * DH;
+        const float *ks = a.k + in_base + (int64_t)nk * a.in_ss + 4 * h32;
 #pragma unroll
         for (int kk = 0; kk < DH; kk += 4) {
-            const f32x4 t = *(const f32x4 *)(ks + kk);
+            const f32x4 t = *(const f32x4 *)(ks + 2 * kk);
 #pragma unroll
             for (int j = 0; j < 4; ++j) kd[kk + j] = t[j];
         }
@@ -927,9 +930,9 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c)
 // 16 x 16 x 4 placement (lane l = n + 16 g): A[m][k] from lane m + 16k,
 // B[k][n] from lane n + 16k, C[m][n] in lane n + 16(m/4), register m % 4.
 //   S^T (keys x queries) = K . Q^T, per 16-key block: lane (n, g) supplies
-//     K[key n][D/4 g + s] and Q[query n][D/4 g + s] at k-step s (each lane
-//     group contracts a contiguous quarter of d);  C: lane (query n, g),
-//     register r <-> key 4g + r of the block.
+//     K[key n][d] and Q[query n][d] at k-step s, d = 16 (s / 4) + 4g + s % 4
+//     (see load_tile);  C: lane (query n, g), register r <-> key 4g + r of
+//     the block.
 //   O^T (d x queries) += V^T . P^T, per 16-key block and k-step r: the
 //     B operand is P^T[key 4g + r][query n], i.e. register r of the S^T
 //     accumulator; the A operand of column block j is V[key 4g + r][E n + j]
@@ -963,27 +966,31 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fwd_split16(FwdArgs a)
     float qr[DQ];
     {
         const int mrow = mq < S ? mq : S - 1;
-        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + DQ * g;
+        const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + 4 * g;
 #pragma unroll
         for (int s4 = 0; s4 < DQ; s4 += 4) {
-            const f32x4 t = *(const f32x4 *)(src + s4);
+            const f32x4 t = *(const f32x4 *)(src + 4 * s4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) qr[s4 + j] = t[j];
         }
     }
 
-    // A 32-key tile: K rows n0 + 16c + n (columns DQ g ..), V rows
-    // n0 + 16c + 4g + r (columns E n ..); rows past S clamped (masked).
+    // A 32-key tile: K rows n0 + 16c + n, V rows n0 + 16c + 4g + r (columns
+    // E n ..); rows past S clamped (masked).  K-step s of lane group g
+    // contracts d = 16 (s / 4) + 4g + s % 4, for Q as for K, so that the
+    // four lanes of a row read 64 contiguous bytes per load: 16 cache lines
+    // per load instruction, where a contiguous quarter of d per lane group
+    // touches up to 64.
     float kr[2][DQ];
     float vr[2][4][E];
     auto load_tile = [&](int n0, float (&kd)[2][DQ], float (&vd)[2][4][E]) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int nk = min(n0 + 16 * c + n, S - 1);
-            const float *ks = a.k + in_base + (int64_t)nk * a.in_ss + DQ * g;
+            const float *ks = a.k + in_base + (int64_t)nk * a.in_ss + 4 * g;
 #pragma unroll
             for (int s4 = 0; s4 < DQ; s4 += 4) {
-                const f32x4 t = *(const f32x4 *)(ks + s4);
+                const f32x4 t = *(const f32x4 *)(ks + 4 * s4);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) kd[c][s4 + j] = t[j];
             }
