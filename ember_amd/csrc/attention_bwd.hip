@@ -285,6 +285,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
     const int stride = (int)gridDim.x;
     int bh = blockIdx.x;
     prefetch(bh);
+    // The first head's rows are waited for here, so that the loop's head,
+    // where this path and the previous iteration's meet, waits only for the
+    // prefetched rows and not for the stores issued after them.
+    wait_vmem();
     for (; bh < nbh; bh += stride) {
         __syncthreads();  // the previous head's products are done with the tiles
         {
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
                 DLs[j] = j < S ? part : 0.0f;
             }
         }
-        if (bh + stride < nbh) prefetch(bh + stride);
+        prefetch(bh + stride < nbh ? bh + stride : bh);  // one path: the last head re-reads itself
         __syncthreads();
 
         // ---- S, dP, P, dS of quadrants w and w + 8 ----
@@ -385,16 +389,21 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
         // non-causal kernel spills 12).
 #pragma unroll 4
         for (int t = 0; t < 8; ++t) kstep(t);
+        // Branch-free bounded stores (rows past S pushed out of the
+        // descriptors' range), so that every path issues the same stores and
+        // the next head's wait for its prefetched rows does not wait for them.
         const int64_t ib = in_base_of(bh);
+        const unsigned range = 4u * (unsigned)((S - 1) * in_ss + 128);
+        const __amdgpu_buffer_rsrc_t rdv = store_rsrc(a.dv + ib, range);
+        const __amdgpu_buffer_rsrc_t rdk = store_rsrc(a.dk + ib, range);
+        const __amdgpu_buffer_rsrc_t rdq = store_rsrc(a.dq + ib, range);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int r = 32 * rb + acc_row(i, h32);
-            if (r < S) {
-                const int64_t off = ib + (int64_t)r * in_ss + col;
-                a.dv[off] = dv[i];
-                a.dk[off] = dk[i] * a.scale;
-                a.dq[off] = dq[i] * a.scale;
-            }
+            const unsigned off = r < S ? 4u * (unsigned)(r * in_ss + col) : kStoreNone;
+            store1_bounded(rdv, off, dv[i]);
+            store1_bounded(rdk, off, dk[i] * a.scale);
+            store1_bounded(rdq, off, dq[i] * a.scale);
         }
     }
 }
@@ -566,10 +575,22 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
             }
             float *__restrict__ dst = o == 0 ? a.dv : (o == 1 ? a.dk : a.dq);
             const float mul = o == 0 ? 1.0f : a.scale;
+            if constexpr (kPersistent) {
+                // Branch-free bounded stores (rows past S pushed out of the
+                // descriptor's range; lds_dma.h): every path issues the same
+                // stores, and the next head's wait skips them.
+                const __amdgpu_buffer_rsrc_t rs = store_rsrc(dst + in_base, 4u * (unsigned)((S - 1) * in_ss + D));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * rb + 4 * g4 + r;
-                if (row < S) dst[in_base + (int64_t)row * in_ss + col] = acc[r] * mul;
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * rb + 4 * g4 + r;
+                    store1_bounded(rs, row < S ? 4u * (unsigned)(row * in_ss + col) : kStoreNone, acc[r] * mul);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * rb + 4 * g4 + r;
+                    if (row < S) dst[in_base + (int64_t)row * in_ss + col] = acc[r] * mul;
+                }
             }
         }
     };
@@ -633,6 +654,10 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
         const int stride = (int)gridDim.x;
         int bh = blockIdx.x;
         prefetch(bh);
+        // The first head's rows are waited for here, so that the loop's
+        // head, where this path and the previous iteration's meet, waits only
+        // for those rows and not for the stores behind them.
+        wait_vmem();
         for (; bh < nbh; bh += stride) {
             __syncthreads();  // the previous head's products are done with LDS
             float part = 0.0f;
@@ -646,7 +671,7 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
                 part += ro[c][0] * rg[c][0] + ro[c][1] * rg[c][1] + ro[c][2] * rg[c][2] + ro[c][3] * rg[c][3];
             }
             put_stats(part, lse_v);
-            if (bh + stride < nbh) prefetch(bh + stride);
+            prefetch(bh + stride < nbh ? bh + stride : bh);  // one path: the last head re-reads itself
             __syncthreads();
             compute(bh);
         }

@@ -1,4 +1,6 @@
-// lds_dma.h -- direct HBM -> LDS copies on gfx950 (not part of the public ABI).
+// lds_dma.h -- buffer-descriptor memory helpers on gfx950 (not part of the
+// public ABI): direct HBM -> LDS copies, wait counts, and bounds-checked
+// stores.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -51,6 +53,28 @@ __device__ __forceinline__ void wait_vmem()
 __device__ __forceinline__ void wait_lds()
 {
     __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+}
+
+// Bounds-checked stores through a buffer descriptor (raw buffer_store): the
+// hardware drops a store whose byte offset (plus its size) passes the
+// descriptor's range.  A lane that must not store passes kStoreNone as its
+// offset, so a masked store needs no branch and every wave issues the same
+// stores on every path.  That matters in the persistent kernels, which load
+// the next head's rows, then store this head's results, then wait for the
+// rows: with the stores under per-row branches the compiler's wait count
+// there can only be vmcnt(0), which waits for the stores as well; with one
+// path it is vmcnt(number of stores).  Ranges stay below kStoreNone.
+constexpr unsigned kStoreNone = 0x80000000u;
+
+// A descriptor over `bytes` bytes from `base` (bytes <= kStoreNone).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t store_rsrc(float *base, unsigned bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void store1_bounded(__amdgpu_buffer_rsrc_t rsrc, unsigned byte_off, float v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), rsrc, byte_off, 0, 0);
 }
 
 }  // namespace ember
