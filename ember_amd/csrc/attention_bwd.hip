@@ -218,6 +218,26 @@ struct ShortLds64 {
     static constexpr int VP = TILE > 2 * R * PSTR ? TILE : 2 * R * PSTR;
 };
 
+// Quadrant e of an N x N grid of 16 x 16 S / dP blocks: row-major, or
+// causally the lower triangle row by row, (0,0), (1,0), (1,1), (2,0), ...
+// Dealing the causal triangle's quadrants in this order to waves
+// e mod NW evens out the SIMDs (waves w and w + 4 share one): at N = 4 and
+// 8 waves, 3, 3, 2, 2 products against 4, 3, 2, 1 for the full grid's
+// quadrants w and w + 8 with the masked ones skipped.
+template <int N, bool CAUSAL>
+__device__ __forceinline__ void quad_of(int e, int &qm, int &qn)
+{
+    if (CAUSAL) {
+        qm = 0;
+#pragma unroll
+        for (int m = 1; m < N; ++m) qm += e >= m * (m + 1) / 2;
+        qn = e - qm * (qm + 1) / 2;
+    } else {
+        qm = e / N;
+        qn = e - qm * N;
+    }
+}
+
 // The kernel is persistent: one workgroup per CU walks heads blockIdx.x,
 // blockIdx.x + gridDim.x, ...  The tiles take the whole LDS, so no second
 // workgroup can overlap one head's HBM traffic with another's products;
@@ -229,6 +249,9 @@ struct ShortLds64 {
 //   prefetched rows -> LDS tiles, delta and lse2 from them;
 //   prefetch the next head's rows; barrier;
 //   S / dP of the quadrants, P / dS, then dV / dK / dQ; store them.
+// Causally the 10 quadrants of the lower triangle are dealt in quad_of's
+// order (SIMDs 3, 3, 2, 2; +3-4 % at S = 48-64 against quadrants w and
+// w + 8 of the full grid, 4, 3, 2, 1).
 // Vector-memory operations retire in issue order and the stores are the
 // last ones of an iteration, so the wait for the prefetched rows at the
 // next iteration's top is vmcnt(stores): it does not wait for the stores.
@@ -315,14 +338,25 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
 
         // ---- S, dP, P, dS of quadrants w and w + 8 ----
         const int l16 = lane & 15, g4 = lane >> 4;
+        // Causal: the 10 quadrants of the lower triangle (quad_of's order)
+        // with products, then (0,1) and (2,3), all masked, which the 32-row
+        // blocks below read and which are written as zeros.
+        constexpr int NQD = CAUSAL ? 12 : 16;
         float pv[2][4], dv4[2][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int quad = w + L::NW * u;
-            const int qm = quad >> 2, qn = quad & 3;
+            const int e = w + L::NW * u;
+            if (e >= NQD) break;
+            int qm, qn;
+            if (CAUSAL && e >= 10) {
+                qm = e == 10 ? 0 : 2;
+                qn = qm + 1;
+            } else {
+                quad_of<4, CAUSAL>(e, qm, qn);
+            }
             const int key = 16 * qn + l16;
             f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
-            if (!CAUSAL || qn <= qm) {
+            if (!CAUSAL || e < 10) {
                 const int arow = (16 * qm + l16) * L::STR + 4 * g4;
                 const int brow = key * L::STR + 4 * g4;
 #pragma unroll
@@ -351,8 +385,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_short_lds64p(BwdArgs a, int n
         __syncthreads();  // every wave is past its dP products: V's space is free
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int quad = w + L::NW * u;
-            const int qm = quad >> 2, qn = quad & 3;
+            const int e = w + L::NW * u;
+            if (e >= NQD) break;
+            int qm, qn;
+            if (CAUSAL && e >= 10) {
+                qm = e == 10 ? 0 : 2;
+                qn = qm + 1;
+            } else {
+                quad_of<4, CAUSAL>(e, qm, qn);
+            }
             const int key = 16 * qn + l16;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -426,8 +467,10 @@ int launch_bwd_short_lds64p(const BwdArgs &args, int nbh)
 // with every product on v_mfma_f32_16x16x4f32 so that the work splits
 // evenly over the waves at any D and R:
 //   wave w: S and dP of the 16 x 16 quadrants w, w + NW, ... of the
-//   (R/16)^2 grid (causal: quadrants above the diagonal are skipped), P and
-//   dS stored transposed ([key][query], rows of R+4) in LDS;
+//   (R/16)^2 grid (causal: quadrants above the diagonal are skipped; at
+//   R = 64 only the 10 of the lower triangle are dealt, in quad_of's order,
+//   so the SIMDs take 3, 3, 2, 2 of them: +6-7 % causal at S = 48-64), P
+//   and dS stored transposed ([key][query], rows of R+4) in LDS;
 //   wave w: the 16 x 16 output blocks w, w + NW, ... of dV, dK (rows: keys)
 //   and dQ (rows: queries), 3 (R/16)(D/16) blocks in all, each contracting
 //   16 queries or keys per group of 4 MFMAs (causal: only the groups that
@@ -447,10 +490,19 @@ struct LdsBwdShape {
     static constexpr int COP = (R * ROWCH + 63) / 64;
     static constexpr int TILE = COP * 256;
     static constexpr int PSTR = R + 4;
-    static constexpr int NQ = (R / 16) * (R / 16) / NW;   // quadrants per wave
     static constexpr int NBO = (R / 16) * (D / 16);        // 16 x 16 blocks per output
     static constexpr int NB = 3 * NBO / NW;                // output blocks per wave
-    static_assert(NQ * NW == (R / 16) * (R / 16) && NB * NW == 3 * NBO, "even split");
+    static_assert(NB * NW == 3 * NBO, "even split");
+    // S / dP quadrants, dealt to the waves in order: wave w takes w,
+    // w + NW, ...  Causal 64-row tiles deal only the lower triangle (the
+    // quadrants the dV / dK / dQ products read) for even SIMDs; at 32 rows
+    // (three workgroups per CU) the full grid with the masked quadrant
+    // written as zeros measured 1 % faster.
+    template <bool CAUSAL> struct Quads {
+        static constexpr bool TRI = CAUSAL && R == 64;
+        static constexpr int N = TRI ? (R / 16) * (R / 16 + 1) / 2 : (R / 16) * (R / 16);
+        static constexpr int PER_WAVE = (N + NW - 1) / NW;
+    };
 };
 
 // R = 64 at D = 64 is persistent (one workgroup per CU walks heads
@@ -505,13 +557,10 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
     // dV, dK, dQ, stored.  Q, K, V, dO and the statistics are in LDS.
     auto compute = [&](int bh) {
         const int64_t in_base = in_base_of(bh);
-#pragma unroll
-        for (int u = 0; u < L::NQ; ++u) {
-            const int quad = w + L::NW * u;
-            const int qm = quad / (R / 16), qn = quad - qm * (R / 16);
+        auto quadrant = [&](int qm, int qn, bool live) {
             const int key = 16 * qn + l16;
             f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
-            if (!CAUSAL || qn <= qm) {
+            if (live) {
                 const int arow = (16 * qm + l16) * L::STR + 4 * g4;
                 const int brow = key * L::STR + 4 * g4;
 #pragma unroll
@@ -535,6 +584,23 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
                 p = vis ? p : 0.0f;
                 PT[key * L::PSTR + qi] = p;
                 DT[key * L::PSTR + qi] = p * (pacc[r] - DLs[qi]);
+            }
+        };
+        if constexpr (L::template Quads<CAUSAL>::TRI) {
+#pragma unroll
+            for (int u = 0; u < L::template Quads<CAUSAL>::PER_WAVE; ++u) {
+                const int e = w + L::NW * u;
+                if (e >= L::template Quads<CAUSAL>::N) break;
+                int qm, qn;
+                quad_of<R / 16, true>(e, qm, qn);
+                quadrant(qm, qn, true);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < (R / 16) * (R / 16) / L::NW; ++u) {
+                const int quad = w + L::NW * u;
+                const int qm = quad / (R / 16), qn = quad - qm * (R / 16);
+                quadrant(qm, qn, !CAUSAL || qn <= qm);
             }
         }
         __syncthreads();
