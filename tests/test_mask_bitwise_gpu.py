@@ -22,8 +22,8 @@ backward (dQ, dK, dV, with O and LSE passed in unchanged):
     of K and V).  Kernels whose dQ is added with atomics run this check in
     deterministic mode, whose per-row sum order is fixed.
 Two tilings (forward): the same head through a split-key kernel (in a
-small launch) and through attn_fwd_kernel, attn_fwd_head or attn_fwd_wave_pair (among 65
-heads) agrees within the north-star tolerance and with the CPU oracle, and
+small launch) and through attn_fwd_kernel (single or paired query blocks), attn_fwd_head or
+attn_fwd_wave_pair (among 65 heads) agrees within the north-star tolerance and with the CPU oracle, and
 both pass the cutoff check above.  Every launch's first and last head are also held to the oracle
 at the north-star tolerance.
 
@@ -122,9 +122,13 @@ FWD_CASES = [
     ("attn_fwd_split", 1, 2, 129, 32),         # D = 32
     ("attn_fwd_kernel", 1, 65, 129, 128),      # 128-query workgroups
     ("attn_fwd_kernel", 1, 65, 300, 64),
-    ("attn_fwd_kernel", 1, 33, 1024, 128),
-    ("attn_fwd_kernel", 1, 40, 1024, 64),
+    ("attn_fwd_kernel", 1, 130, 1024, 128),    # block pairs would exceed one round: single blocks
+    ("attn_fwd_kernel", 1, 200, 1024, 64),
     ("attn_fwd_kernel", 1, 65, 200, 32),
+    ("attn_fwd_kernel_pairs", 1, 33, 1024, 128),  # blocks nqb - 1 - p and p per workgroup
+    ("attn_fwd_kernel_pairs", 1, 40, 1024, 64),
+    ("attn_fwd_kernel_pairs", 1, 40, 640, 64),    # odd nqb: the middle block alone
+    ("attn_fwd_kernel_pairs", 1, 30, 600, 32),
     ("attn_fwd_head", 1, 65, 128, 64),         # persistent whole-head workgroups, D = 64
     ("attn_fwd_head", 1, 300, 80, 64),         # more heads than CUs: each workgroup walks several
     ("attn_fwd_head", 1, 70, 113, 64),
@@ -171,8 +175,8 @@ def test_forward_mask_is_bit_exact(kernel, B, H, S, D):
 
 @pytest.mark.parametrize("S,D,H1,alone,other", [
     (300, 128, 1, "attn_fwd_split16", "attn_fwd_kernel"),
-    (1024, 64, 5, "attn_fwd_split", "attn_fwd_kernel"),
-    (1024, 64, 1, "attn_fwd_split16_w8", "attn_fwd_kernel"),
+    (1024, 64, 5, "attn_fwd_split", "attn_fwd_kernel_pairs"),
+    (1024, 64, 1, "attn_fwd_split16_w8", "attn_fwd_kernel_pairs"),
     (128, 64, 1, "attn_fwd_split16", "attn_fwd_head"),
     (96, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
     (100, 128, 1, "attn_fwd_split16", "attn_fwd_wave_pair"),
