@@ -69,7 +69,7 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c)
 //     operand of the k-step that contracts query 4g + r; lane (n, g) reads
 //     dO[4g + r][64h + 4n + j] as the B operand of column block 4h + j;
 //   dQ = dS K: lane (n, g) reads dS[n][16c + 4g + j] and K^T[d][16c + 4g + j].
-template <int D, bool CAUSAL, int DQ>
+template <int D, bool CAUSAL, int DQ, bool PAIRK>
 __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
 {
     typedef W16Shape<D> L;
@@ -84,14 +84,21 @@ __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
     const int n = lane & 15, g = lane >> 4;
     const int S = a.S;
     const int nch = (S + 15) >> 4;
-    const int BH = (int)(gridDim.x / nkb);
-    const int kb = blockIdx.x / BH;  // ascending: the longest causal walks first
-    const int bh = blockIdx.x - kb * BH;
+    // PAIRK (causal, atomic dQ): key blocks p and nkb - 1 - p of a head, one
+    // after the other, so that every workgroup walks about 2 nch - 4 nkb
+    // query chunks (the middle block of an odd nkb alone, dispatched last).
+    static_assert(!PAIRK || DQ == kDqAtomic, "the ordered dQ follows single key blocks");
+    const int per_head = PAIRK ? (nkb + 1) / 2 : nkb;
+    const int BH = (int)(gridDim.x / per_head);
+    const int kb0 = blockIdx.x / BH;  // ascending: the longest causal walks first
+    const int bh = blockIdx.x - kb0 * BH;
     const int b = bh / a.H;
     const int hh = bh - b * a.H;
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
     const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
+    // Key block kb of head bh.
+    auto run = [&](int kb) {
     const int c0 = CPW * kb;                   // the workgroup's first key chunk
     const int kc = c0 + w;                     // this wave's key chunk
     const bool kvalid = 16 * kc < S;           // the chunk holds keys of the sequence
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
 
     // dK (scaled) and dV of this wave's keys: register r of block 4h + j
     // holds key 16 kc + 4g + r, column 64h + 4n + j.
-    if (!kvalid) return;
+    if (kvalid) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int key = 16 * kc + 4 * g + r;
@@ -328,6 +335,20 @@ __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
             *(f32x4 *)(dvrow + 64 * h) = vo;
         }
     }
+    }
+    };
+    if constexpr (PAIRK) {
+        for (int pi = 0; pi < 2; ++pi) {
+            const int kb = pi == 0 ? kb0 : nkb - 1 - kb0;
+            if (pi == 1) {
+                if (kb == kb0) break;
+                __syncthreads();  // every wave is done with the first block's K^T and dS
+            }
+            run(kb);
+        }
+    } else {
+        run(kb0);
+    }
 }
 
 template <bool CAUSAL>
@@ -340,10 +361,25 @@ int launch_w16(const BwdArgs &args, int64_t rows_pad, int nbh)
     if (!launch_ok("attn_bwd_pre")) return EMBER_ERR_DEVICE;
     const int nkb = (args.S + W16Shape<D>::KB - 1) / W16Shape<D>::KB;
     const dim3 grid((unsigned)(nkb * nbh));
-    if (!args.order)
-        hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqAtomic>), grid, dim3(256), 0, 0, args, nkb);
-    else
-        hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqOrdered>), grid, dim3(256), 0, 0, args, nkb);
+    if (!args.order) {
+        // Causal launches whose key-block pairs all fit one round of resident
+        // workgroups take the blocks in pairs of about equal walks: measured
+        // +4 % at B4 H16 S = 1024, +8-9 % at B2 H16 S = 2048 and B1 H16
+        // S = 4096, +-0 at B8 H16 S = 1024; at S = 512 (short walks, which do
+        // not cover the second block's prologue) -2.5 %, so from 16 blocks.
+        if constexpr (CAUSAL) {
+            const int ncu = device_cu_count();
+            const int64_t pairs = (int64_t)(nkb + 1) / 2 * nbh;
+            if (nkb >= 16 && pairs <= (int64_t)(ncu > 0 ? ncu : 256) * 4) {
+                hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqAtomic, true>), dim3((unsigned)pairs), dim3(256), 0,
+                                   0, args, nkb);
+                return launch_ok("attn_bwd_w16_pairs") ? EMBER_OK : EMBER_ERR_DEVICE;
+            }
+        }
+        hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqAtomic, false>), grid, dim3(256), 0, 0, args, nkb);
+    } else {
+        hipLaunchKernelGGL((attn_bwd_w16<D, CAUSAL, kDqOrdered, false>), grid, dim3(256), 0, 0, args, nkb);
+    }
     return launch_ok("attn_bwd_w16") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 

@@ -140,6 +140,7 @@ def test_s128_backward_many_heads(B, H, S, D, causal, pads, hpads):
     (1, 12, 700, 64, True, [12, 4], [0, 3]),
     (2, 20, 513, 64, False, [0, 0], [0, 2]),
     (1, 8, 1000, 64, True, [32, 12], [1, 1]),
+    (1, 3, 1025, 64, True, [4, 4], [1, 1]),     # 17 key blocks: pairs, the middle one alone
     (4, 24, 129, 64, True, [4, 0], [0, 1]),
 ])
 def test_w16_backward_many_heads(B, H, S, D, causal, pads, hpads):
@@ -147,7 +148,8 @@ def test_w16_backward_many_heads(B, H, S, D, causal, pads, hpads):
     chunks, four workgroups per CU, one dS buffer and two barriers per step)
     with up to 480 workgroups, ragged S (partial last 16-row chunks and
     64-key blocks with keys past S), both masks and padded strides on both
-    triples."""
+    triples; causal S = 1000 and 1025 (16 and 17 key blocks) take the key
+    blocks in pairs per workgroup."""
     _run(700 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 

@@ -170,7 +170,8 @@ def test_mask_tests_reach_every_attention_kernel():
                     if "launch_ok(" in line:
                         names.update(re.findall(r'"(attn_\w+)"', line))
     helpers = {"attn_bwd_pre", "attn_bwd_dq_reduce"}   # row statistics and the slab sum: no mask
-    assert names - helpers == {c[0] for c in M.FWD_CASES} | {c[0] for c in M.BWD_CASES}
+    assert names - helpers == ({c[0] for c in M.FWD_CASES} | {c[0] for c in M.BWD_CASES}
+                                | {c[0] for c in M.BWD_ATOMIC_CASES})
     assert len(names) >= 13
 
 

@@ -20,7 +20,9 @@ backward (dQ, dK, dV, with O and LSE passed in unchanged):
     (key j > i must contribute exactly zero to query i), and dK, dV rows
     <= c_h as well (with O and LSE fixed, key j's gradient reads only row j
     of K and V).  Kernels whose dQ is added with atomics run this check in
-    deterministic mode, whose per-row sum order is fixed.
+    deterministic mode, whose per-row sum order is fixed; a launch that runs
+    only with atomic dQ (key-block pairs) holds dQ to the reordering of a
+    sum (1e-5) instead.
 Two tilings (forward): the same head through a split-key kernel (in a
 small launch) and through attn_fwd_kernel (single or paired query blocks), attn_fwd_head or
 attn_fwd_wave_pair (among 65 heads) agrees within the north-star tolerance and with the CPU oracle, and
@@ -272,6 +274,51 @@ def test_backward_mask_is_bit_exact(kernel, B, H, S, D, det, restore_mode):
                or _rows_equal(dv, dv3, cut, True))
         assert err is None, f"{kernel} dQ: {err}"
 
+    for f in (0, B * H - 1):
+        b, h = divmod(f, H)
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        refs = oracle.attention_bwd(q[sl], k[sl], v[sl], o[sl], lse[sl], d_o[sl], True)
+        for name, got, ref in zip(("dQ", "dK", "dV"), (dq, dk, dv), refs):
+            np.testing.assert_allclose(got[sl], ref, err_msg=f"{name} head {f}", **TOL)
+
+
+# (kernel, B, H, S, D): launches that run only with atomic dQ (the ordered
+# dQ of deterministic mode follows single key blocks).
+BWD_ATOMIC_CASES = [
+    ("attn_bwd_w16_pairs", 1, 6, 1024, 64),   # key blocks p and nkb - 1 - p per workgroup
+    ("attn_bwd_w16_pairs", 1, 5, 1030, 64),   # odd nkb: the middle block alone
+]
+
+
+@pytest.mark.parametrize("kernel,B,H,S,D", BWD_ATOMIC_CASES)
+def test_backward_mask_atomic_dq(kernel, B, H, S, D, restore_mode):
+    """As test_backward_mask_is_bit_exact, with dQ added by atomics in
+    whatever order the hardware runs them: dK and dV bitwise, dQ rows at or
+    before the cutoff equal to within the reordering of a sum (1e-5; one
+    leaked key would move a row by about P * |dP - delta| * |K| * scale,
+    about 1e-4 here)."""
+    rng = np.random.default_rng(S * 19 + D + H)
+    q, k, v, d_o = (_rand((B, H, S, D), rng) for _ in range(4))
+    o, lse = G.attention_fwd(q, k, v, True)
+    capi.set_deterministic(False)
+    G.say(f"backward mask (atomic dQ) {kernel} B={B} H={H} S={S} D={D}")
+    log = []
+    dq, dk, dv = G.attention_bwd(q, k, v, o, lse, d_o, True, log=log)
+    assert kernel in log, log
+    for cut in _cutoff_rounds(B * H, S, S * 3 + D):
+        q2, d_o2, o2 = (_replace_before(x, cut, rng) for x in (q, d_o, o))
+        lse2 = _replace_before(lse, cut, rng, scale=0.25, add=True)
+        _, dk2, dv2 = G.attention_bwd(q2, k, v, o2, lse2, d_o2, True)
+        err = _rows_equal(dk, dk2, cut, False) or _rows_equal(dv, dv2, cut, False)
+        assert err is None, f"{kernel} dK/dV: {err}"
+        k3, v3 = _replace_after(k, cut, rng), _replace_after(v, cut, rng)
+        dq3, dk3, dv3 = G.attention_bwd(q, k3, v3, o, lse, d_o, True)
+        err = _rows_equal(dk, dk3, cut, True) or _rows_equal(dv, dv3, cut, True)
+        assert err is None, f"{kernel} dK/dV (keys replaced): {err}"
+        a, b3 = dq.reshape(B * H, S, D), dq3.reshape(B * H, S, D)
+        for h, c in enumerate(cut):
+            np.testing.assert_allclose(b3[h, :c + 1], a[h, :c + 1], rtol=1e-5, atol=1e-5,
+                                       err_msg=f"{kernel} dQ head {h} cutoff {c}")
     for f in (0, B * H - 1):
         b, h = divmod(f, H)
         sl = (slice(b, b + 1), slice(h, h + 1))
