@@ -134,6 +134,19 @@ def test_s128_backward_many_heads(B, H, S, D, causal, pads, hpads):
 
 
 @pytest.mark.parametrize("B,H,S,D,causal,pads,hpads", [
+    (2, 12, 1024, 64, True, [4, 12], [1, 0]),   # 8 query blocks: pairs; backward key-block pairs too
+    (1, 33, 640, 128, True, [12, 4], [0, 3]),   # 5 query blocks: the middle one alone
+    (3, 10, 600, 32, True, [32, 0], [1, 1]),
+])
+def test_paired_query_blocks(B, H, S, D, causal, pads, hpads):
+    """Causal launches of 128-query workgroups whose block pairs fit one
+    round of resident workgroups (attn_fwd_kernel_pairs: query blocks
+    nqb - 1 - p and p per workgroup, the second's first K tile copied during
+    the first's last tile), with padded strides on both triples."""
+    _run(900 + B + H + S + D, B, H, S, D, causal, pads, hpads)
+
+
+@pytest.mark.parametrize("B,H,S,D,causal,pads,hpads", [
     (2, 60, 200, 64, True, [0, 0], [0, 0]),
     (1, 40, 321, 64, False, [4, 12], [1, 0]),
     (3, 30, 257, 64, True, [0, 32], [3, 1]),
