@@ -965,6 +965,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fwd_split16(FwdArgs a)
     constexpr int E = D / 16;   // column blocks of O^T; floats of a V row per lane
     __shared__ float part[NW * D * 16];  // O^T partials [w][d][query]
     __shared__ float mst[NW * 16], lst[NW * 16];
+    __shared__ float qs[NW == 4 ? 16 * (D + 4) : 1];  // the block's Q rows, read once for all waves
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -982,8 +983,27 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fwd_split16(FwdArgs a)
     const int mq = m0 + n;
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
 
+    // Four waves: the block's Q rows (16 x D) are read once, 16 bytes per
+    // thread, into LDS ahead of the key tiles' loads, and every wave takes
+    // its operand from there after one barrier (each wave reading them
+    // itself made a quarter of a CU's loads repeats): -3.5 to -5 % at
+    // S = 128-300.  Eight waves read their own (the barrier measured +5 %
+    // at config 1).
+    constexpr bool kQShared = NW == 4;
+    constexpr int QPIECES = 16 * D / 4;
+    constexpr int QPT = (QPIECES + 64 * NW - 1) / (64 * NW);  // pieces per thread
+    f32x4 qpiece[QPT];
     float qr[DQ];
-    {
+    if constexpr (kQShared) {
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+            // Unconditional (a thread past the pieces re-reads one), so that
+            // the wait for them below counts exactly the key tile's loads.
+            const int pc = (tid + 64 * NW * u) % QPIECES;
+            const int qrow = pc / (D / 4), qcol = 4 * (pc - qrow * (D / 4));
+            qpiece[u] = *(const f32x4 *)(a.q + in_base + (int64_t)min(m0 + qrow, S - 1) * a.in_ss + qcol);
+        }
+    } else {
         const int mrow = mq < S ? mq : S - 1;
         const float *src = a.q + in_base + (int64_t)mrow * a.in_ss + 4 * g;
 #pragma unroll
@@ -1035,7 +1055,26 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_fwd_split16(FwdArgs a)
     const int kend = CAUSAL ? min(S, m0 + 16) : S;
     const int ntiles = (kend + 31) / 32;
     int t = w;
-    if (t < ntiles) load_tile(32 * t, kr, vr);
+    if constexpr (kQShared) {
+        load_tile(32 * min(t, ntiles - 1), kr, vr);  // a wave without a tile re-reads the last (unused)
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+            // Every thread writes (one past the pieces writes the same bits
+            // to the same place), so the load is not sunk behind the tile's.
+            const int pc = (tid + 64 * NW * u) % QPIECES;
+            const int qrow = pc / (D / 4), qcol = 4 * (pc - qrow * (D / 4));
+            *(f32x4 *)&qs[qrow * (D + 4) + qcol] = qpiece[u];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s4 = 0; s4 < DQ; s4 += 4) {
+            const f32x4 tq = *(const f32x4 *)&qs[n * (D + 4) + 4 * s4 + 4 * g];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qr[s4 + j] = tq[j];
+        }
+    } else {
+        if (t < ntiles) load_tile(32 * t, kr, vr);
+    }
     for (; t < ntiles; t += NW) {
         const int n0 = 32 * t;
         float kn[2][DQ];
