@@ -85,6 +85,8 @@ def test_random_short_sequence_many_heads(seed):
 
 
 @pytest.mark.parametrize("B,H,S,D,causal,pads,hpads", [
+    (4, 250, 20, 64, True, [4, 0], [1, 2]),     # D = 64, S < 32: persistent 32-row workgroups, 1000 heads
+    (2, 400, 32, 64, False, [0, 12], [0, 1]),   # non-causal S = 32: the same, 800 heads
     (1, 257, 32, 128, False, [0, 0], [0, 0]),
     (3, 171, 9, 128, True, [4, 12], [1, 0]),
     (5, 206, 32, 128, True, [0, 32], [3, 1]),
@@ -102,7 +104,8 @@ def test_short_backward_walks_many_heads(B, H, S, D, causal, pads, hpads):
     padded strides on both triples: at S <= 32 the one-head workgroups that
     share a CU must not disturb each other's LDS tiles; at 32 < S <= 64 with
     D = 64 or 128 one persistent workgroup per CU walks several heads, each
-    prefetched during the previous one (a ragged last pass included)."""
+    prefetched during the previous one (a ragged last pass included), as do
+    three 32-row workgroups per CU at D = 64 for S < 32 and non-causally."""
     _run(300 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 

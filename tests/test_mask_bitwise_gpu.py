@@ -225,6 +225,7 @@ BWD_CASES = [
     ("attn_bwd_short_lds64p", 1, 5, 50, 128, False),
     ("attn_bwd_lds16_r32", 1, 8, 32, 64, False),        # S <= 32, D <= 64
     ("attn_bwd_lds16_r32", 1, 8, 25, 32, False),
+    ("attn_bwd_lds16_r32", 1, 1000, 25, 64, False),   # persistent (S < 32 at D = 64), > 768 heads
     ("attn_bwd_lds16_r64", 1, 300, 64, 64, False),      # persistent at D = 64
     ("attn_bwd_lds16_r64", 1, 6, 48, 32, False),
     ("attn_bwd_s128", 1, 400, 72, 128, False),          # persistent, odd chunk count
