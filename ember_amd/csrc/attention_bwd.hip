@@ -33,179 +33,23 @@ int device_cus(int *out)
     return *out > 0 ? EMBER_OK : record_error(EMBER_ERR_DEVICE, "hipDeviceGetAttribute(CU count)");
 }
 
-// Short sequences at D = 128 (S <= 32): one workgroup of 4 waves per head,
-// the head's Q, K, V and dO staged in LDS by direct HBM -> LDS copies
-// (coalesced 1 KiB copies, no registers), so every operand the products
-// read row-by-lane comes from LDS instead of from scattered 16-byte global
-// loads.  Per head:
-//   copies of Q, K, V, dO (padded rows of D+4 floats); meanwhile each wave
-//   forms delta = <dO, O> for 8 rows from coalesced global reads of O and dO
-//   (8 lanes per row) and lse2 = lse * log2(e);
-//   wave w: S and dP of the 16 x 16 quadrant (queries 16(w/2).., keys
-//   16(w%2)..) on v_mfma_f32_16x16x4f32 over all of D (a causal head skips
-//   the quadrant above the diagonal), then P and dS of the quadrant, stored
-//   transposed ([key][query]) in LDS;
-//   wave w: columns 32w..32w+31 of dV = P^T dO, dK = scale dS^T Q and
-//   dQ = scale dS K on v_mfma_f32_32x32x2f32 (contraction over the 32
-//   queries or keys in the order q = (s & 7) + 8h + 16(s >> 3) for k-step s
-//   and lane half h, which puts the two lane halves' LDS rows 8 apart, in
-//   disjoint banks).
-// Rows past S are copied as row S-1 and carry lse2 = +inf (P = 0), delta = 0.
-// Two workgroups per CU (79 KB of LDS each).
-struct ShortLds {
-    static constexpr int D = 128;
-    static constexpr int STR = D + 4;                 // padded tile row (floats)
-    static constexpr int ROWCH = STR / 4;             // 16-byte chunks per padded row
-    static constexpr int COP = (kBq * ROWCH + 63) / 64;  // 1 KiB copies per tile
-    static constexpr int TILE = COP * 256;            // floats reserved per tile
-    static constexpr int PSTR = kBq + 4;              // padded row of P^T / dS^T
-};
-
-template <bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_short_lds(BwdArgs a)
-{
-    typedef ShortLds L;
-    constexpr int D = L::D;
-    __shared__ float tiles[4 * L::TILE];  // Q, K, V, dO
-    __shared__ float PT[kBq * L::PSTR], DT[kBq * L::PSTR];
-    __shared__ float L2s[kBq], DLs[kBq];
-    float *__restrict__ Qs = tiles;
-    float *__restrict__ Ks = tiles + L::TILE;
-    float *__restrict__ Vs = tiles + 2 * L::TILE;
-    float *__restrict__ Gs = tiles + 3 * L::TILE;
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int bh = blockIdx.x;
-    const int b = bh / a.H;
-    const int hh = bh - b * a.H;
-    const int S = a.S;
-    const int in_ss = (int)a.in_ss, out_ss = (int)a.out_ss;  // < 2^24 (checked on the host)
-    const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
-    const int64_t out_base = (int64_t)b * a.out_sb + (int64_t)hh * a.out_sh;
-
-    // ---- copies: copy t of a tile fills chunks 64t..64t+63 (row p / ROWCH,
-    // chunk p % ROWCH); the padding chunk and the slack past the tile re-read
-    // the tile's first chunk ----
-    {
-        const __amdgpu_buffer_rsrc_t rq = dma_rsrc(a.q + in_base);
-        const __amdgpu_buffer_rsrc_t rk = dma_rsrc(a.k + in_base);
-        const __amdgpu_buffer_rsrc_t rv = dma_rsrc(a.v + in_base);
-        const __amdgpu_buffer_rsrc_t rg = dma_rsrc(a.dout + out_base);
-#pragma unroll
-        for (int t = w; t < L::COP; t += kWaves) {
-            const int p = 64 * t + lane;
-            int r = p / L::ROWCH;
-            const int c = p - r * L::ROWCH;
-            const bool real = r < kBq && c < D / 4;
-            r = r < S ? r : S - 1;
-            const unsigned oi = real ? 4u * (unsigned)(r * in_ss + 4 * c) : 0u;
-            const unsigned og = real ? 4u * (unsigned)(r * out_ss + 4 * c) : 0u;
-            dma16_buf(rq, oi, Qs + 256 * t);
-            dma16_buf(rk, oi, Ks + 256 * t);
-            dma16_buf(rv, oi, Vs + 256 * t);
-            dma16_buf(rg, og, Gs + 256 * t);
-        }
-    }
-    // ---- row statistics of rows 8w..8w+7: 8 lanes per row ----
-    {
-        const int j = 8 * w + (lane >> 3);
-        const int s8 = lane & 7;
-        const int jr = j < S ? j : S - 1;
-        const float *__restrict__ orow = a.o + out_base + (int64_t)jr * out_ss;
-        const float *__restrict__ grow = a.dout + out_base + (int64_t)jr * out_ss;
-        float part = 0.0f;
-#pragma unroll
-        for (int it = 0; it < D / 32; ++it) {
-            const f32x4 o4 = *(const f32x4 *)(orow + 32 * it + 4 * s8);
-            const f32x4 g4 = *(const f32x4 *)(grow + 32 * it + 4 * s8);
-            part += o4[0] * g4[0] + o4[1] * g4[1] + o4[2] * g4[2] + o4[3] * g4[3];
-        }
-        part += __shfl_xor(part, 1);
-        part += __shfl_xor(part, 2);
-        part += __shfl_xor(part, 4);
-        if (s8 == 0) {
-            L2s[j] = j < S ? a.lse[(int64_t)bh * S + j] * kLog2e : INFINITY;
-            DLs[j] = j < S ? part : 0.0f;
-        }
-    }
-    wait_vmem();
-    __syncthreads();
-
-    // ---- S, dP, P, dS of quadrant (qm, qn) ----
-    {
-        const int qm = w >> 1, qn = w & 1;
-        const int l16 = lane & 15, g4 = lane >> 4;
-        const int key = 16 * qn + l16;
-        f32x4 sacc = {0.f, 0.f, 0.f, 0.f}, pacc = {0.f, 0.f, 0.f, 0.f};
-        if (!CAUSAL || qn <= qm) {
-            const int arow = (16 * qm + l16) * L::STR + 4 * g4;
-            const int brow = key * L::STR + 4 * g4;
-#pragma unroll
-            for (int c0 = 0; c0 < D; c0 += 16) {
-                const f32x4 qf = *(const f32x4 *)&Qs[arow + c0];
-                const f32x4 kf = *(const f32x4 *)&Ks[brow + c0];
-                const f32x4 gf = *(const f32x4 *)&Gs[arow + c0];
-                const f32x4 vf = *(const f32x4 *)&Vs[brow + c0];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[j], kf[j], sacc, 0, 0, 0);
-                    pacc = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[j], vf[j], pacc, 0, 0, 0);
-                }
-            }
-        }
-        // C[m][n] of the quadrant: lane (n = l16, g4), register r: m = 4 g4 + r.
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int qi = 16 * qm + 4 * g4 + r;
-            float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], a.c, -L2s[qi]));
-            const bool vis = key < S && (!CAUSAL || key <= qi);
-            p = vis ? p : 0.0f;
-            PT[key * L::PSTR + qi] = p;
-            DT[key * L::PSTR + qi] = p * (pacc[r] - DLs[qi]);
-        }
-    }
-    __syncthreads();
-
-    // ---- columns 32w.. of dV, dK, dQ ----
-    const int h32 = lane >> 5, l32 = lane & 31;
-    const int col = 32 * w + l32;
-    f32x16 dv = zero16(), dk = zero16(), dq = zero16();
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        // k-steps s = 4t..4t+3 contract rows q = (s & 7) + 8 h32 + 16 (s >> 3)
-        const int q0 = 4 * (t & 1) + 8 * h32 + 16 * (t >> 1);
-        const f32x4 pt = *(const f32x4 *)&PT[l32 * L::PSTR + q0];
-        const f32x4 dt = *(const f32x4 *)&DT[l32 * L::PSTR + q0];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int q = q0 + j;
-            dv = mfma_32x32x2(pt[j], Gs[q * L::STR + col], dv);
-            dk = mfma_32x32x2(dt[j], Qs[q * L::STR + col], dk);
-            dq = mfma_32x32x2(DT[q * L::PSTR + l32], Ks[q * L::STR + col], dq);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = acc_row(i, h32);
-        if (r < S) {
-            const int64_t off = in_base + (int64_t)r * in_ss + col;
-            a.dv[off] = dv[i];
-            a.dk[off] = dk[i] * a.scale;
-            a.dq[off] = dq[i] * a.scale;
-        }
-    }
-}
-
-// 32 < S <= 64 at D = 128: the same scheme with 64-row tiles and a
-// workgroup of 8 waves (Q, K, dO and V take 132 KB of LDS: one per CU).
-// P^T and dS^T (64 x 68 floats each) overlay the V tile once every wave is
-// past its dP products, so P and dS wait in registers across one barrier.
+// 32 < S <= 64 at D = 128: a workgroup of 8 waves stages one head's Q, K,
+// dO and V in LDS as 64 padded rows of D+4 floats (132 KB: one workgroup
+// per CU), forms delta = <dO, O> per row and lse2 = lse * log2(e) while
+// staging, and never leaves the CU for intermediate results.  Rows past S
+// are staged as row S-1 and carry lse2 = +inf (P = 0), delta = 0.  P^T and
+// dS^T (64 x 68 floats each) overlay the V tile once every wave is past its
+// dP products, so P and dS wait in registers across one barrier.
 //   wave w: S / dP quadrants w and w + 8 of the 4 x 4 grid of 16 x 16
-//   quadrants (a causal head skips those above the diagonal);
-//   wave w: rows 32(w/4).. and columns 32(w%4).. of dV, dK and dQ, over the
-//   64 queries / keys (a causal head skips the half that is all zeros: keys
-//   32.. see only queries 32.., queries 0..31 only keys 0..31).
+//   quadrants on v_mfma_f32_16x16x4f32 over all of D (causally: the lower
+//   triangle, dealt as below);
+//   wave w: rows 32(w/4).. and columns 32(w%4).. of dV, dK and dQ on
+//   v_mfma_f32_32x32x2f32 over the 64 queries / keys (a causal head skips
+//   the half that is all zeros: keys 32.. see only queries 32.., queries
+//   0..31 only keys 0..31), contracting in the order
+//   q = 4 (s & 1) + 8 h + 16 (s >> 1) + j for k-step s, lane half h and
+//   MFMA j, which puts the two lane halves' LDS rows 8 apart, in disjoint
+//   banks.
 struct ShortLds64 {
     static constexpr int D = 128;
     static constexpr int R = 64;                         // rows per tile
@@ -463,11 +307,11 @@ int launch_bwd_short_lds64p(const BwdArgs &args, int nbh)
 }
 
 
-// Short sequences at D <= 64 (S <= R, R = 32 or 64 rows): one workgroup of
-// R/8 waves per head, the head's Q, K, V, dO staged in LDS by direct copies
-// into padded rows (D+4 floats), as attn_bwd_short_lds does at D = 128, but
-// with every product on v_mfma_f32_16x16x4f32 so that the work splits
-// evenly over the waves at any D and R:
+// Short sequences (S <= R; R = 32 or 64 rows at D <= 64, R = 32 at
+// D = 128): one workgroup of R/8 waves per head, the head's Q, K, V, dO
+// staged in LDS in padded rows (D+4 floats; rows past S staged as row S-1,
+// with lse2 = +inf and delta = 0), every product on v_mfma_f32_16x16x4f32
+// so that the work splits evenly over the waves at any D and R:
 //   wave w: S and dP of the 16 x 16 quadrants w, w + NW, ... of the
 //   (R/16)^2 grid (causal: quadrants above the diagonal are skipped; at
 //   R = 64 only the 10 of the lower triangle are dealt, in quad_of's order,
@@ -482,8 +326,8 @@ int launch_bwd_short_lds64p(const BwdArgs &args, int nbh)
 // [k][n] lane n + 16k: with k = 4 g + j (g = lane / 16, MFMA j of a group
 // of 4), P^T / dS^T rows are read as 128-bit segments, the other operand
 // one float per lane from rows 4 apart (disjoint banks for rows of D+4 or
-// R+4 floats).  R = 32: 46 KB of LDS at D = 64 (three workgroups per CU);
-// R = 64: 104 KB (one per CU).
+// R+4 floats).  R = 32: 46 KB of LDS at D = 64 (three workgroups per CU),
+// 79 KB at D = 128 (two); R = 64: 104 KB at D = 64 (one per CU).
 template <int D, int R>
 struct LdsBwdShape {
     static constexpr int NW = R / 8;
@@ -517,13 +361,16 @@ struct LdsBwdShape {
 // R = 32 at D = 64 (three workgroups per CU) takes the persistent form
 // (PERS, three per CU) for S < 32 and non-causally: +27 % at S = 17, +5 %
 // at S = 25, +3.7 % non-causal at S = 32; causal S = 32 measured -1.5 %
-// and keeps one workgroup per head.
+// and keeps one workgroup per head.  R = 32 at D = 128 is persistent with
+// two workgroups per CU (S <= 32; against a one-head-per-workgroup kernel
+// with direct HBM -> LDS copies and 32 x 32 products: +14 % at S = 17,
+// +8 % at S = 25, +1.6 % causal and +2.8 % non-causal at S = 32).
 template <int D, int R, bool CAUSAL, bool PERS>
 __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs a, int nbh)
 {
     typedef LdsBwdShape<D, R> L;
     constexpr bool kPersistent = PERS;
-    static_assert(!PERS || D == 64, "the persistent form is laid out for D = 64");
+    static_assert(!PERS || D == 64 || (D == 128 && R == 32), "persistent forms: D = 64, or D = 128 with 32 rows");
     constexpr int CH = D / 32;  // 16-byte chunks per lane and row
     __shared__ float tiles[4 * L::TILE];  // Q, K, V, dO
     __shared__ float PT[R * L::PSTR], DT[R * L::PSTR];
@@ -756,29 +603,22 @@ __global__ __launch_bounds__(R * 8, R == 32 ? 2 : 1) void attn_bwd_lds16(BwdArgs
 template <int D, int R, bool CAUSAL>
 int launch_bwd_lds16(const BwdArgs &args, int nbh)
 {
-    if constexpr (D == 64) {
-        if (R == 64 || !CAUSAL || args.S < 32) {
+    if constexpr (D == 64 || (D == 128 && R == 32)) {
+        if (D == 128 || R == 64 || !CAUSAL || args.S < 32) {
             int ncu = 0;
             const int st = device_cus(&ncu);
             if (st != EMBER_OK) return st;
-            const int slots = ncu * (R == 32 ? 3 : 1);
+            const int slots = ncu * (D == 128 ? 2 : (R == 32 ? 3 : 1));
             const int grid = nbh < slots ? nbh : slots;
             hipLaunchKernelGGL((attn_bwd_lds16<D, R, CAUSAL, true>), dim3((unsigned)grid), dim3(R * 8), 0, 0, args,
                                nbh);
             return launch_ok(R == 32 ? "attn_bwd_lds16_r32" : "attn_bwd_lds16_r64") ? EMBER_OK : EMBER_ERR_DEVICE;
         }
     }
-    if constexpr (!(D == 64 && R == 64))  // (always persistent)
+    if constexpr (!((D == 64 && R == 64) || D == 128))  // (always persistent)
         hipLaunchKernelGGL((attn_bwd_lds16<D, R, CAUSAL, false>), dim3((unsigned)nbh), dim3(R * 8), 0, 0, args,
                            nbh);
     return launch_ok(R == 32 ? "attn_bwd_lds16_r32" : "attn_bwd_lds16_r64") ? EMBER_OK : EMBER_ERR_DEVICE;
-}
-
-template <bool CAUSAL>
-int launch_bwd_short_lds(const BwdArgs &args, int nbh)
-{
-    hipLaunchKernelGGL((attn_bwd_short_lds<CAUSAL>), dim3((unsigned)nbh), dim3(kThreads), 0, 0, args);
-    return launch_ok("attn_bwd_short_lds") ? EMBER_OK : EMBER_ERR_DEVICE;
 }
 
 
@@ -880,10 +720,11 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
 
     // S <= 64: a workgroup stages one head's Q, K, V and dO in LDS and forms
     // the row statistics itself (no scratch, no atomics):
-    // attn_bwd_short_lds (S <= 32) and attn_bwd_short_lds64p at D = 128,
-    // attn_bwd_lds16 with 32- or 64-row tiles at D <= 64; where a workgroup
-    // fills a CU's LDS (64-row tiles at D = 64 and 128) it is persistent
-    // and prefetches the next head into registers.  Measured with 2^20
+    // attn_bwd_lds16 with 32- or 64-row tiles at D <= 64 and 32-row tiles
+    // at D = 128 (S <= 32), attn_bwd_short_lds64p at D = 128 (S <= 64); the
+    // 64-row kernels at D = 64 and 128, which fill a CU's LDS, and most
+    // 32-row launches at D = 64 and 128 are persistent and prefetch the next
+    // head into registers.  Measured with 2^20
     // query rows: 4.6-4.9 TB/s at S = 32 and 3.7-4.3 TB/s at S = 64 (causal),
     // where the register-fed kernels they replaced (one wave per head or
     // per key block, rows read one per lane from HBM) moved 2.8-3.5 and
@@ -924,8 +765,8 @@ int attention_bwd_rows(const float *q, const float *k, const float *v, const flo
             case 3: return launch_bwd_lds16<32, 32, true>(sa, nbh);
             case 4: return launch_bwd_lds16<64, 32, false>(sa, nbh);
             case 5: return launch_bwd_lds16<64, 32, true>(sa, nbh);
-            case 8: return launch_bwd_short_lds<false>(sa, nbh);
-            case 9: return launch_bwd_short_lds<true>(sa, nbh);
+            case 8: return launch_bwd_lds16<128, 32, false>(sa, nbh);
+            case 9: return launch_bwd_lds16<128, 32, true>(sa, nbh);
             case 10: return launch_bwd_lds16<32, 64, false>(sa, nbh);
             case 11: return launch_bwd_lds16<32, 64, true>(sa, nbh);
             case 12: return launch_bwd_lds16<64, 64, false>(sa, nbh);

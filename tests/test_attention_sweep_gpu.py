@@ -101,11 +101,12 @@ def test_random_short_sequence_many_heads(seed):
 ])
 def test_short_backward_walks_many_heads(B, H, S, D, causal, pads, hpads):
     """S <= 64 with hundreds to thousands of heads (257 to 2560, ragged S),
-    padded strides on both triples: at S <= 32 the one-head workgroups that
-    share a CU must not disturb each other's LDS tiles; at 32 < S <= 64 with
-    D = 64 or 128 one persistent workgroup per CU walks several heads, each
+    padded strides on both triples: at S <= 32 the workgroups that share a
+    CU must not disturb each other's LDS tiles; at 32 < S <= 64 with D = 64
+    or 128 one persistent workgroup per CU walks several heads, each
     prefetched during the previous one (a ragged last pass included), as do
-    three 32-row workgroups per CU at D = 64 for S < 32 and non-causally."""
+    three 32-row workgroups per CU at D = 64 for S < 32 and non-causally,
+    and two per CU at D = 128 for S <= 32."""
     _run(300 + B + H + S + D, B, H, S, D, causal, pads, hpads)
 
 

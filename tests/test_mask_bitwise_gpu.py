@@ -219,8 +219,8 @@ def test_two_tilings_same_mask(S, D, H1, alone, other):
 # (kernel, B, H, S, D, deterministic dQ needed): each shape reaches the named
 # backward kernel.
 BWD_CASES = [
-    ("attn_bwd_short_lds", 1, 8, 32, 128, False),       # S <= 32, D = 128
-    ("attn_bwd_short_lds", 1, 5, 17, 128, False),
+    ("attn_bwd_lds16_r32", 1, 8, 32, 128, False),       # S <= 32, D = 128: persistent, two per CU
+    ("attn_bwd_lds16_r32", 1, 600, 17, 128, False),     # > 512 heads: a second pass
     ("attn_bwd_short_lds64p", 1, 300, 64, 128, False),  # persistent, > 256 heads
     ("attn_bwd_short_lds64p", 1, 5, 50, 128, False),
     ("attn_bwd_lds16_r32", 1, 8, 32, 64, False),        # S <= 32, D <= 64
