@@ -1248,7 +1248,7 @@ __global__ __launch_bounds__(512, D == 64 ? 2 : 1) void attn_fwd_head(FwdArgs a)
     const int qrow_c = min(mq, S - 1);
 
     f32x4 kp[PER / 4], vp[PER / 4], qp[DQ / 4];
-    auto prefetch = [&](int bh) {
+    auto prefetch_kv = [&](int bh) {
         const int b = bh / a.H;
         const int64_t base = (int64_t)b * a.in_sb + (int64_t)(bh - b * a.H) * a.in_sh;
         const float *ks = a.k + base + (int64_t)srow_c * a.in_ss + PER * spart;
@@ -1258,11 +1258,17 @@ __global__ __launch_bounds__(512, D == 64 ? 2 : 1) void attn_fwd_head(FwdArgs a)
             kp[i] = *(const f32x4 *)(ks + 4 * i);
             vp[i] = *(const f32x4 *)(vs + 4 * i);
         }
-        if (active) {
-            const float *qs = a.q + base + (int64_t)qrow_c * a.in_ss + DQ * g;
+    };
+    auto prefetch_q = [&](int bh) {
+        const int b = bh / a.H;
+        const int64_t base = (int64_t)b * a.in_sb + (int64_t)(bh - b * a.H) * a.in_sh;
+        const float *qs = a.q + base + (int64_t)qrow_c * a.in_ss + DQ * g;
 #pragma unroll
-            for (int i = 0; i < DQ / 4; ++i) qp[i] = *(const f32x4 *)(qs + 4 * i);
-        }
+        for (int i = 0; i < DQ / 4; ++i) qp[i] = *(const f32x4 *)(qs + 4 * i);
+    };
+    auto prefetch = [&](int bh) {
+        prefetch_kv(bh);
+        if (active) prefetch_q(bh);
     };
 
     const int nbh = a.nbh;
@@ -1281,9 +1287,14 @@ __global__ __launch_bounds__(512, D == 64 ? 2 : 1) void attn_fwd_head(FwdArgs a)
 #pragma unroll
             for (int j = 0; j < 4; ++j) qr[4 * i + j] = qp[i][j];
         __syncthreads();
-        // The next head's loads are issued after the barrier, so that no
-        // wave waits at it for the others' issue (+1-3 % at S = 72-112).
-        if (bh + (int)gridDim.x < nbh) prefetch(bh + gridDim.x);
+        // The next head's K and V rows are requested after the barrier, so
+        // that no wave waits at it for the others' issue (+1-3 % at
+        // S = 72-112); its Q rows only after this wave's last key chunk
+        // (+2-7 % at S = 80-128: fewer loads queued while every wave starts
+        // its products, and the waves, whose chunk counts differ, issue
+        // them at different times).
+        const bool has_next = bh + (int)gridDim.x < nbh;
+        if (has_next) prefetch_kv(bh + gridDim.x);
         if (!active) continue;
 
         f32x4 oacc[E];
@@ -1339,6 +1350,7 @@ __global__ __launch_bounds__(512, D == 64 ? 2 : 1) void attn_fwd_head(FwdArgs a)
                 }
             }
         }
+        if (has_next) prefetch_q(bh + gridDim.x);
 
         float ltot = lrun + __shfl_xor(lrun, 16);
         ltot += __shfl_xor(ltot, 32);
