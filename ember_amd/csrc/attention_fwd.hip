@@ -369,15 +369,17 @@ __global__ __launch_bounds__(kThreads, D == 64 ? 3 : 2) void attn_fwd_kernel(Fwd
 // products in this HBM-bound regime.  PAIR (64 < S <= 128, D >= 64; see
 // launch_fwd): one wave per pair of blocks p and nqb - 1 - p of a head,
 // taken one after the other, so that causally every wave has the same
-// number of key tiles; the second block's Q rows are copied into the slice
-// during the first block's last tile, once its K reads are done (+0.5-1.6 %
-// at S = 80-128).  Each wave stages its Q tile, then
-// each 32-key K tile, through a private padded LDS slice with coalesced
-// copies (buffer_load ... lds: an MFMA operand puts one row per lane, which
-// read straight from HBM would touch 64 lines per load), and loads V
-// straight into registers in operand order (already row-contiguous across
-// lanes).  Per tile: S^T = K.Q^T, the online softmax of attn_fwd_kernel,
+// number of key tiles.  Each wave stages its Q tile, then each 32-key K
+// tile, through a private padded LDS slice with coalesced copies
+// (buffer_load ... lds: an MFMA operand puts one row per lane, which read
+// straight from HBM would touch 64 lines per load), and loads V straight
+// into registers in operand order (already row-contiguous across lanes).
+// Per tile: S^T = K.Q^T, the online softmax of attn_fwd_kernel,
 // O^T += V^T.P^T.  Rows past the sequence end re-read row S-1 (masked).
+// Once a tile's K reads are done, the slice takes the next K tile, or after
+// a pair's first block the second block's Q rows, while the softmax and
+// the V products run (+0.5-3 % at S = 48-128; the V loads, into registers
+// still in use, wait for the tile's start).
 template <int D>
 struct WaveSlice {
     static constexpr int STR = D + 4;                // padded row (floats)
@@ -458,9 +460,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
     float mrun = -INFINITY, lrun = 0.0f;
 
     const int kend = CAUSAL ? min(S, m0 + 32) : S;
+    wait_lds();  // this wave's reads of Q are complete before the copy overwrites them
+    stage(a.k + in_base, 0);
     for (int n0 = 0; n0 < kend; n0 += 32) {
-        wait_lds();  // this wave's earlier reads of buf are complete before the copy overwrites it
-        stage(a.k + in_base, n0);
         VT vr[16];   // V operand for k-step i: V[n0 + acc_row(i, h32)][DB*l32 .. +DB)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -476,8 +478,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
 #pragma unroll
             for (int j = 0; j < 4; ++j) sacc = mfma_32x32x2(kf[j], qr[kk + j], sacc);
         }
-        if (next_qb >= 0 && n0 + 32 >= kend) {
+        if (n0 + 32 < kend) {
             wait_lds();  // this wave's reads of the K tile are complete
+            stage(a.k + in_base, n0 + 32);
+        } else if (next_qb >= 0) {
+            wait_lds();  // the same, before the next block's Q rows
             stage(a.q + in_base, 32 * next_qb);
         }
         const bool need_mask = n0 + 32 > S || (CAUSAL && n0 + 31 > m0);
