@@ -379,7 +379,8 @@ __global__ __launch_bounds__(kThreads, D == 64 ? 3 : 2) void attn_fwd_kernel(Fwd
 // Once a tile's K reads are done, the slice takes the next K tile, or after
 // a pair's first block the second block's Q rows, while the softmax and
 // the V products run (+0.5-3 % at S = 48-128; the V loads, into registers
-// still in use, wait for the tile's start).
+// still in use, wait for the tile's start, and are waited for only by the
+// V products: +1-4 % at S = 32-128).
 template <int D>
 struct WaveSlice {
     static constexpr int STR = D + 4;                // padded row (floats)
@@ -470,7 +471,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
             nv = nv < S ? nv : S - 1;
             vr[i] = *(const VT *)(vb + (int64_t)nv * a.in_ss + DB * l32);
         }
-        wait_vmem();
+        // The K tile, copied before these 16 V loads, has landed; the V
+        // rows are waited for one by one before the products that read them
+        // (the compiler's waits), so the S products and the softmax run
+        // while they arrive.
+        wait_vmem_n<16>();
         f32x16 sacc = zero16();
 #pragma unroll
         for (int kk = 0; kk < DH; kk += 4) {
