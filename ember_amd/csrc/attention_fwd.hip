@@ -13,9 +13,9 @@
 // while V of tile t is multiplied; two barriers per tile.
 // Short sequences (S <= 64, HBM-bound) use one wave per 32-query block
 // instead, with no barriers (attn_fwd_wave, D >= 64), or pack heads
-// (attn_fwd_packed: D = 32, and non-causal D = 64 at S > 32): S <= 32 puts
-// 4 heads in a workgroup (one per wave, tiles of 32 keys) and S <= 64 puts
-// 2 (two waves each), so that no wave idles and every wave keeps loading.
+// (attn_fwd_packed, D = 32): S <= 32 puts 4 heads in a workgroup (one per
+// wave, tiles of 32 keys) and S <= 64 puts 2 (two waves each), so that no
+// wave idles and every wave keeps loading.
 // 64 < S <= 96, and causal S <= 128, at D >= 64 take attn_fwd_wave with one
 // wave per pair of query blocks.
 //
@@ -1482,20 +1482,17 @@ int launch_fwd(FwdArgs args, int64_t nbh)
     }
     // S <= 64: the wave kernel at D = 128 (4.7 TB/s at S = 32 and 4.0 at
     // S = 64, where the packed kernel moves 3.8 and 2.9) and at D = 64
-    // (causal +9-13 % at S = 32, +25 % at S = 48, +5-11 % at S = 64,
-    // non-causal +6 % at S = 32; 8192-32768 heads), except non-causal
-    // D = 64 at 32 < S <= 64 (-1.5 %) and D = 32, which keep the packed
-    // kernel.
+    // (against the packed kernel: causal +9-13 % at S = 32, +25 % at S = 48,
+    // +5-11 % at S = 64; non-causal +6 % at S = 32, +25-33 % at S = 33-48,
+    // equal at S = 64; 8192-32768 heads); D = 32 keeps the packed kernel.
     if constexpr (D >= 64) {
-        if (D == 128 || CAUSAL || args.S <= 32) {
-            args.nqb = (args.S + 31) / 32;
-            const int64_t items = (int64_t)args.nqb * nbh;
-            hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, false>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
-                               dim3(kThreads), 0, 0, args);
-            return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
-        }
+        args.nqb = (args.S + 31) / 32;
+        const int64_t items = (int64_t)args.nqb * nbh;
+        hipLaunchKernelGGL((attn_fwd_wave<D, CAUSAL, false>), dim3((unsigned)((items + kWaves - 1) / kWaves)),
+                           dim3(kThreads), 0, 0, args);
+        return launch_ok("attn_fwd_wave") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
-    if constexpr (D < 128) {
+    if constexpr (D == 32) {
         args.nqb = 1;
         if (args.S <= 32) {
             hipLaunchKernelGGL((attn_fwd_packed<D, CAUSAL, 4, 32>), dim3((unsigned)((nbh + 3) / 4)),
@@ -1506,7 +1503,7 @@ int launch_fwd(FwdArgs args, int64_t nbh)
                            dim3(kThreads), 0, 0, args);
         return launch_ok("attn_fwd_packed_hp2") ? EMBER_OK : EMBER_ERR_DEVICE;
     }
-    return EMBER_OK;  // not reached: D = 128 always takes the wave kernel above
+    return EMBER_OK;  // not reached: every head size returns above
 }
 
 }  // namespace
