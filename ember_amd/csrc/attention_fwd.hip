@@ -362,7 +362,7 @@ __global__ __launch_bounds__(kThreads, D == 64 ? 3 : 2) void attn_fwd_kernel(Fwd
     }
 }
 
-// S <= 64 (D = 128; D = 64 but non-causal S > 32, see launch_fwd): one
+// S <= 64 (D = 64 and 128, see launch_fwd): one
 // wave per (head, 32-query block), four independent
 // waves per workgroup (consecutive query blocks of a head share one) and no
 // barriers, so that two waves per SIMD overlap one's copies with another's
@@ -417,7 +417,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_wave(FwdArgs a)
     const int in_ss = (int)a.in_ss;  // < 2^24 (checked on the host)
     const int64_t in_base = (int64_t)b * a.in_sb + (int64_t)hh * a.in_sh;
     const float *__restrict__ vb = a.v + in_base;
-    // Query block qb of head bh.
     // Query block qb of head bh; q_ready: its Q rows are already being
     // copied into buf; next_qb >= 0: the block that follows, whose Q rows
     // are copied into buf during this block's last tile, once its K reads
