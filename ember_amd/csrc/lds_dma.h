@@ -63,8 +63,11 @@ __device__ __forceinline__ void wait_lds()
 // the next head's rows, then store this head's results, then wait for the
 // rows: with the stores under per-row branches the compiler's wait count
 // there can only be vmcnt(0), which waits for the stores as well; with one
-// path it is vmcnt(number of stores).  Ranges stay below kStoreNone.
-constexpr unsigned kStoreNone = 0x80000000u;
+// path it is vmcnt(number of stores).  Ranges stay below kStoreNone: the
+// kernels that use these stores cover at most 64 rows of a head, so a range
+// is at most 4 * (63 * (2^24 - 1) + 128) bytes (row strides are below 2^24
+// floats, checked on the host), 4227858692 < 0xFFFFFF00.
+constexpr unsigned kStoreNone = 0xFFFFFF00u;
 
 // A descriptor over `bytes` bytes from `base` (bytes <= kStoreNone).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t store_rsrc(float *base, unsigned bytes)

@@ -6,6 +6,8 @@ bitwise through invariants that any leak across the mask would break.
 All calls go through the C ABI (libember_amd.so).
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -292,6 +294,59 @@ def test_row_stride_at_the_guard_edge():
     st = L.attention_bwd(o.ptr, o.ptr, o.ptr, o.ptr, lse.ptr, ddo.ptr, o.ptr, o.ptr, o.ptr, B, H, S, D,
                          scale, 1, *too_far, *out_st)
     assert st == 1 and L.ember_get_last_error() == 1
+
+
+@pytest.mark.parametrize("S,D,kernel", [(50, 64, "attn_bwd_lds16_r64"), (50, 128, "attn_bwd_short_lds64p")])
+def test_short_backward_row_stride_at_the_guard_edge(S, D, kernel):
+    """Row stride 2^24 - 4 floats at S <= 64, where the backward runs a
+    persistent LDS-staged kernel whose stores are branch-free and bounded:
+    a store for a row past S (rows 50..63 of the 64-row tile) takes an
+    offset past the store descriptor's range, and at this stride the range
+    is 4 * (49 * (2^24 - 4) + D) bytes, past 2^31.  One head; q / k / v side
+    by side in each row, the gradients in a buffer of the same layout filled
+    with SENTINEL first: every gradient matches the oracle and the padding
+    of every row (the 256 floats after its data) is untouched."""
+    from ember_amd import capi
+    from ember_amd.capi import DeviceArray
+
+    B, H = 1, 1
+    ss = (1 << 24) - 4
+    width = 3 * H * D
+    rows = _rand((S, H, 3, D), 960 + D)
+    d_o = _rand((B, H, S, D), 961 + D)
+    q, k, v = (np.ascontiguousarray(rows[:, :, i].transpose(1, 0, 2))[None] for i in range(3))
+    scale = G.scale_for(D)
+    L = capi.lib()
+    L.constant.argtypes = [ctypes.c_float, ctypes.c_void_p, ctypes.c_int]
+    G.say(f"short backward, row stride {ss} floats: S={S} D={D} (two {S * ss * 4 / 2**30:.1f} GiB buffers)")
+    buf, gbuf = DeviceArray((S * ss,)), DeviceArray((S * ss,))
+    L.constant(G.SENTINEL, gbuf.ptr, S * ss)
+    for r in range(S):
+        L.copy_to_device(buf.ptr + 4 * r * ss, np.ascontiguousarray(rows[r]).ctypes.data, 4 * width)
+    capi.check(what="copy_to_device")
+    o, lse = DeviceArray((B, H, S, D)), DeviceArray((B, H, S))
+    ddo = DeviceArray.from_numpy(d_o)
+    in_st, out_st = (S * ss, 3 * D, ss), capi.contiguous_strides(B, H, S, D)
+    base, gb = buf.ptr, gbuf.ptr
+    capi.check(L.attention_fwd(base, base + 4 * D, base + 8 * D, o.ptr, lse.ptr, B, H, S, D, scale, 1,
+                               *in_st, *out_st), "attention_fwd")
+    capi.launch_log_reset()
+    capi.check(L.attention_bwd(base, base + 4 * D, base + 8 * D, o.ptr, lse.ptr, ddo.ptr,
+                               gb, gb + 4 * D, gb + 8 * D, B, H, S, D, scale, 1, *in_st, *out_st),
+               "attention_bwd")
+    assert kernel in capi.launch_log()
+    span = width + 256
+    g = np.empty((S, span), np.float32)
+    for r in range(S):
+        L.copy_from_device(g[r].ctypes.data, gb + 4 * r * ss, 4 * span)
+    capi.check(what="copy_from_device")
+    assert np.all(g[:, width:] == G.SENTINEL)
+    g = g[:, :width].reshape(S, H, 3, D)
+    o_ref, lse_ref = oracle.attention_fwd(q, k, v, True, scale)
+    refs = oracle.attention_bwd(q, k, v, o_ref, lse_ref, d_o, True, scale)
+    for i, (name, ref) in enumerate(zip(("dq", "dk", "dv"), refs)):
+        np.testing.assert_allclose(g[:, :, i].transpose(1, 0, 2)[None], ref, err_msg=name, **TOL)
+    del buf, gbuf
 
 
 # ------------------------------------------------------------ long sequences
