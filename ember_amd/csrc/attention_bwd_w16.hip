@@ -256,7 +256,8 @@ __global__ __launch_bounds__(256, 4) void attn_bwd_w16(BwdArgs a, int nkb)
             const int row = 16 * qc + 4 * g + r;
             if (row < S) {
 #pragma unroll
-                for (int q = 0; q < QB; ++q) unsafeAtomicAdd(dqb + row * in_ss + 16 * q, acc[q][r] * a.scale);
+                for (int q = 0; q < QB; ++q)
+                    unsafeAtomicAdd(dqb + (int64_t)row * in_ss + 16 * q, acc[q][r] * a.scale);  // row * in_ss may pass 2^31
             }
         }
     };

@@ -242,17 +242,21 @@ def test_packed_qkv_layout(S, D):
     np.testing.assert_allclose(g[:, :, 0].transpose(0, 2, 1, 3), dq_ref, rtol=1e-5, atol=1e-6)
 
 
-def test_row_stride_at_the_guard_edge():
+@pytest.mark.parametrize("S", [96, 160])
+def test_row_stride_at_the_guard_edge(S):
     """Row stride 2^24 - 4 floats, the largest the entry points accept (rows
     64 MiB apart): the forward's HBM->LDS copies address a 64-key tile's
     rows with 32-bit byte offsets up to 4 * 63 * (2^24 - 4), past 2^31.
     65 heads of S = 96 make the forward take its one-head-per-workgroup
-    kernel; q / k / v of a head sit side by side in each row.  A stride of
-    2^24 is rejected with EMBER_ERR_INVALID_ARGUMENT before any launch."""
+    kernel and the backward attn_bwd_s128; at S = 160 the backward takes
+    attn_bwd_w16, whose dQ rows past 127 sit more than 2^31 floats from the
+    head's first.  q / k / v of a head sit side by side in each row.  A
+    stride of 2^24 is rejected with EMBER_ERR_INVALID_ARGUMENT before any
+    launch."""
     from ember_amd import capi
     from ember_amd.capi import DeviceArray
 
-    B, H, S, D = 1, 65, 96, 64
+    B, H, D = 1, 65, 64
     ss = (1 << 24) - 4
     width = 3 * H * D
     rows = _rand((S, H, 3, D), 950)
